@@ -1,0 +1,167 @@
+/*
+ * q3vl_int8.h -- C ABI of the MI355X (gfx950) int8 group-quantized matmul
+ * library libq3vl_int8.so.
+ *
+ * It replaces the int8 branch of the reference engine's matmul entry point
+ *   void linear(const void *A, const void *B, const void *B_scale,
+ *               const void *bias, const void *bias_scale, void *C,
+ *               size_t M, size_t N, size_t K, bool B_transpose,
+ *               DType::Type ta, DType::Type tb, DType::Type tb_scale,
+ *               DType::Type tc, bool group_quantized, size_t group_size)
+ * (matmul/include/cpu_wrapper.hpp:10-16, matmul/src/cpu_wrapper.cpp:308-357)
+ * and its consumers on the decode path: SwiGLU (layers/src/text_layer.cpp:
+ * 420-434), the lm_head classifier_gemm (layers/src/text_layer.cpp:302-314)
+ * and greedy_decode (tokenizer/src/utils.cpp:34-44).
+ *
+ * Conventions (identical to the reference's int8 path):
+ *   A  fp32 [M, K] row-major activations;
+ *   W  int8 [N, K] row-major weights (the reference's B with
+ *      mat_B_transpose = true);
+ *   S  fp32 [N, K/gs] row-major group scales, S[n*K/gs + g];
+ *   C  fp32 [M, N], overwritten.
+ * Activations are quantized per row and per K-group to int16 with an RMS
+ * scale; int32 group sums are exact; the fp32 results reproduce the
+ * reference's operation order bit for bit:
+ *   M==1 && N>=1024 && K>=1024 : per-lane FMA chains + fixed 8-lane tree
+ *                                (cpu_f32a_i8f32sb_f32c_avx2.cpp:122-224);
+ *   otherwise                  : acc = fma(float(G)*a_s, w_s, acc) per group
+ *                                (cpu_f32a_i8f32sb_f32c_avx2.cpp:477-662).
+ *
+ * All pointers passed to compute entry points are DEVICE pointers (HIP
+ * allocations visible to the current device). Every call is asynchronous on
+ * `stream` (a hipStream_t; NULL = the null stream) and returns a status code;
+ * q3vl_last_error() gives the message of this thread's last failure.
+ *
+ * Shape support: K % group_size == 0. M <= 8 runs the HBM-bound GEMV kernels
+ * (group_size in {16,32,64,128,256}, K <= 8192, K % 16 == 0); M > 8 runs the
+ * matrix-core GEMM (group_size in {32,64,128}, K % 64 == 0). A and W must be
+ * 16-byte aligned.
+ *
+ * Workspace: entry points that need scratch device memory take `workspace`
+ * and `workspace_bytes` (>= q3vl_workspace_bytes()). Passing NULL makes the
+ * library use its own per-device buffer, grown on demand with hipMalloc
+ * (not allowed while the stream is being captured into a HIP graph; capture
+ * callers pass their own workspace). Calls sharing one workspace must be
+ * ordered on one stream.
+ */
+#ifndef Q3VL_INT8_H
+#define Q3VL_INT8_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void *q3vl_stream; /* hipStream_t */
+
+enum q3vl_status {
+    Q3VL_OK = 0,
+    Q3VL_ERR_INVALID_ARGUMENT = 1, /* null / misaligned pointer, bad shape   */
+    Q3VL_ERR_UNSUPPORTED = 2,      /* dtype combination or shape not served  */
+    Q3VL_ERR_HIP = 3,              /* a HIP runtime call failed              */
+    Q3VL_ERR_OUT_OF_MEMORY = 4     /* workspace or registry allocation failed */
+};
+
+/* DType values of the reference (utils/include/tensor.hpp:38). */
+enum q3vl_dtype {
+    Q3VL_DTYPE_FP32 = 0,
+    Q3VL_DTYPE_INT32 = 1,
+    Q3VL_DTYPE_FP16 = 2,
+    Q3VL_DTYPE_INT8 = 3,
+    Q3VL_DTYPE_INT4 = 4
+};
+
+/* Message of this thread's last failing call ("" if none). */
+const char *q3vl_last_error(void);
+/* ABI version of this header (bumped on any signature change). */
+int q3vl_abi_version(void);
+#define Q3VL_ABI_VERSION 1
+
+/* Scratch bytes needed by q3vl_linear_i8* / q3vl_lm_head_argmax for a shape. */
+size_t q3vl_workspace_bytes(size_t M, size_t N, size_t K, size_t group_size);
+
+/* Dispatch check of linear() (matmul/src/cpu_wrapper.cpp:320-357): returns
+ * Q3VL_OK when (ta, tb, tb_scale, tc, has_bias, group_quantized, B_transpose)
+ * is the int8 group-quantized combination this library serves, else
+ * Q3VL_ERR_UNSUPPORTED with a message naming the combination. */
+int q3vl_check_dtypes(int ta, int tb, int tb_scale, int tc, int has_bias,
+                      int group_quantized, int b_transpose);
+
+/* 1 when (M, N, K) takes the reference's M=1 lane-ordered GEMV
+ * (cpu_f32a_i8f32sb_f32c_avx2.cpp:464), 0 for the general path. */
+int q3vl_uses_lane_path(size_t M, size_t N, size_t K);
+
+/* Activation quantizer (cpu_f32a_i8f32sb_f32c_avx2.cpp:135-177):
+ * A [M,K] fp32 -> q [M,K] int16, a_s [M,K/gs] fp32. */
+int q3vl_quantize_rows(const float *A, int16_t *q, float *a_s, size_t M,
+                       size_t K, size_t group_size, q3vl_stream stream);
+
+/* The int8 branch of linear() (cpu_wrapper.cpp:339-348): C = A W^T. */
+int q3vl_linear_i8(const float *A, const int8_t *W, const float *S, float *C,
+                   size_t M, size_t N, size_t K, size_t group_size,
+                   void *workspace, size_t workspace_bytes, q3vl_stream stream);
+
+/* As q3vl_linear_i8, also writing the exact int32 group accumulators
+ * G[(m*N + n)*(K/gs) + g] = sum_{k in g} q[m,k]*W[n,k] (a parity probe; the
+ * GEMM variant that writes G is slower). */
+int q3vl_linear_i8_groups(const float *A, const int8_t *W, const float *S,
+                          float *C, int32_t *G, size_t M, size_t N, size_t K,
+                          size_t group_size, void *workspace,
+                          size_t workspace_bytes, q3vl_stream stream);
+
+/* Up to three linears over the same activation in one pass (the decode
+ * step's q/k/v projections, model/src/forward.cpp:506-528): C[i] = A W[i]^T,
+ * each with the numerics linear() gives its own (M, N[i], K). */
+int q3vl_linear_i8_multi(const float *A, size_t M, size_t K, size_t group_size,
+                         int count, const int8_t *const *W,
+                         const float *const *S, float *const *C,
+                         const size_t *N, void *workspace,
+                         size_t workspace_bytes, q3vl_stream stream);
+
+/* gate and up projections plus swiglu (model/src/forward.cpp:623-642,
+ * layers/src/text_layer.cpp:420-434) in one pass:
+ * H[m,n] = silu(A Wg^T)[m,n] * (A Wu^T)[m,n], Wg/Wu [N,K]. */
+int q3vl_linear_i8_swiglu(const float *A, const int8_t *Wg, const float *Sg,
+                          const int8_t *Wu, const float *Su, float *H,
+                          size_t M, size_t N, size_t K, size_t group_size,
+                          void *workspace, size_t workspace_bytes,
+                          q3vl_stream stream);
+
+/* lm_head (classifier_gemm, layers/src/text_layer.cpp:302-314) fused with
+ * greedy_decode (tokenizer/src/utils.cpp:34-44): ids[m] = first index of the
+ * maximum of row m of A W^T (W [V,K]). logits may be NULL (not stored) for
+ * M <= 8. */
+int q3vl_lm_head_argmax(const float *A, const int8_t *W, const float *S,
+                        float *logits, int32_t *ids, size_t M, size_t V,
+                        size_t K, size_t group_size, void *workspace,
+                        size_t workspace_bytes, q3vl_stream stream);
+
+/* greedy_decode over each row of logits [M, V]. */
+int q3vl_argmax_rows(const float *logits, int32_t *ids, size_t M, size_t V,
+                     void *workspace, size_t workspace_bytes,
+                     q3vl_stream stream);
+
+/* swiglu (layers/src/text_layer.cpp:420-434): gate = silu(gate) * up. */
+int q3vl_swiglu(float *gate, const float *up, size_t n, q3vl_stream stream);
+
+/* ---- weight registry for host-pointer callers (the drop-in linear()).
+ * The reference hands linear() mmapped host pointers to weights and scales
+ * (model/src/load_model.cpp:146-181); the registry uploads a weight once and
+ * maps its host address to device copies (256-byte aligned). */
+int q3vl_weight_register(const int8_t *host_W, const float *host_S, size_t N,
+                         size_t K, size_t group_size, const int8_t **dev_W,
+                         const float **dev_S);
+/* Device copies of a registered host weight; Q3VL_ERR_INVALID_ARGUMENT if
+ * host_W is not registered. */
+int q3vl_weight_lookup(const void *host_W, const int8_t **dev_W,
+                       const float **dev_S);
+int q3vl_weight_release(const void *host_W);
+int q3vl_weight_release_all(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* Q3VL_INT8_H */

@@ -1,0 +1,465 @@
+// capi.cpp -- extern "C" entry points of libq3vl_int8.so (include/q3vl_int8.h).
+//
+// Validates arguments, turns the reference's fprintf+exit(1) failure modes
+// into status codes, manages scratch memory and the host-weight registry, and
+// dispatches to the gfx950 kernels exactly as the reference's shape dispatch
+// (matmul/src/cpu_f32a_i8f32sb_f32c_avx2.cpp:464-475) selects its numerics.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "q3vl_int8.h"
+#include "q3vl_kernels.hpp"
+
+using namespace q3vl;
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char *what) {
+    return fail(Q3VL_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+#define Q3VL_HIP(call, what)                          \
+    do {                                              \
+        hipError_t e_ = (call);                       \
+        if (e_ != hipSuccess) return hip_fail(e_, what); \
+    } while (0)
+
+inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+inline bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+
+constexpr size_t kMaxGemvParts = 8192;  // >= grid of any GEMV launch
+constexpr int kGemmArgmaxParts = 64;    // argmax partials per row after a GEMM
+
+bool gs_ok_gemv(size_t gs) { return gs == 16 || gs == 32 || gs == 64 || gs == 128 || gs == 256; }
+bool gs_ok_gemm(size_t gs) { return gs == 32 || gs == 64 || gs == 128; }
+
+// ---- workspace layout
+struct WsLayout {
+    size_t parts_val = 0, parts_idx = 0;  // argmax partials
+    size_t aq = 0, as = 0;                // GEMM: fp16 activations, transposed scales
+    size_t logits = 0;                    // lm_head M > 8 without caller logits
+    size_t total = 0;
+    int lda_s = 0;
+};
+
+WsLayout layout(size_t M, size_t N, size_t K, size_t gs) {
+    WsLayout L;
+    size_t off = 0;
+    const size_t mm = M ? M : 1;
+    L.parts_val = off;
+    off += align256(kMaxGemvParts * mm * sizeof(float));
+    L.parts_idx = off;
+    off += align256(kMaxGemvParts * mm * sizeof(int32_t));
+    if (M > 8) {
+        const size_t Kg = gs ? K / gs : 0;
+        L.lda_s = (int)((M + 3) & ~(size_t)3);
+        L.aq = off;
+        off += align256(M * K * 2);
+        L.as = off;
+        off += align256(Kg * (size_t)L.lda_s * 4);
+        L.logits = off;
+        off += align256(M * N * 4);
+    }
+    L.total = off;
+    return L;
+}
+
+// ---- library-owned default workspace (per device, grow-only)
+struct DefaultWs {
+    std::mutex mu;
+    std::vector<void *> buf;
+    std::vector<size_t> size;
+};
+DefaultWs g_ws;
+
+int resolve_ws(void *user, size_t user_bytes, size_t need, char **out) {
+    if (user) {
+        if (user_bytes < need)
+            return fail(Q3VL_ERR_INVALID_ARGUMENT,
+                        "workspace too small: %zu bytes given, %zu needed", user_bytes, need);
+        if (((uintptr_t)user & 255u) != 0)
+            return fail(Q3VL_ERR_INVALID_ARGUMENT, "workspace must be 256-byte aligned");
+        *out = static_cast<char *>(user);
+        return Q3VL_OK;
+    }
+    int dev = 0;
+    Q3VL_HIP(hipGetDevice(&dev), "hipGetDevice");
+    std::lock_guard<std::mutex> lk(g_ws.mu);
+    if ((size_t)dev >= g_ws.buf.size()) {
+        g_ws.buf.resize(dev + 1, nullptr);
+        g_ws.size.resize(dev + 1, 0);
+    }
+    if (g_ws.size[dev] < need) {
+        if (g_ws.buf[dev]) {
+            // Work queued on any stream may still read the old buffer.
+            Q3VL_HIP(hipDeviceSynchronize(), "hipDeviceSynchronize");
+            Q3VL_HIP(hipFree(g_ws.buf[dev]), "hipFree(workspace)");
+            g_ws.buf[dev] = nullptr;
+            g_ws.size[dev] = 0;
+        }
+        size_t sz = need < (1u << 20) ? (1u << 20) : need;
+        void *p = nullptr;
+        if (hipMalloc(&p, sz) != hipSuccess)
+            return fail(Q3VL_ERR_OUT_OF_MEMORY, "workspace hipMalloc(%zu) failed", sz);
+        g_ws.buf[dev] = p;
+        g_ws.size[dev] = sz;
+    }
+    *out = static_cast<char *>(g_ws.buf[dev]);
+    return Q3VL_OK;
+}
+
+int check_common(const void *A, const void *W, const void *S, size_t M, size_t N,
+                 size_t K, size_t gs) {
+    if (gs == 0 || K % gs != 0)
+        return fail(Q3VL_ERR_INVALID_ARGUMENT, "K=%zu must be a multiple of group_size=%zu", K, gs);
+    if (M && N && K && (!A || !W || !S))
+        return fail(Q3VL_ERR_INVALID_ARGUMENT, "null A/W/S pointer");
+    if ((A && !aligned16(A)) || (W && !aligned16(W)))
+        return fail(Q3VL_ERR_INVALID_ARGUMENT, "A and W must be 16-byte aligned");
+    if (M > 0x7fffffff || N > 0x7fffffff || K > 0x7fffffff || N * K > 0x7fffffffULL ||
+        M * K > 0x7fffffffULL)
+        return fail(Q3VL_ERR_UNSUPPORTED, "shape too large (M=%zu N=%zu K=%zu)", M, N, K);
+    return Q3VL_OK;
+}
+
+bool gemv_path_ok(size_t M, size_t K, size_t gs) {
+    return M <= 8 && K % 16 == 0 && K / 16 <= 512 && gs_ok_gemv(gs);
+}
+
+// Shared-activation runner: segments ride one GEMV launch (M <= 8) or one
+// quantization followed by one GEMM per segment (M > 8).
+int run_linear(const float *A, int nseg, const int8_t *const *W, const float *const *S,
+               float *const *C, int32_t *const *G, const size_t *Ns, size_t M, size_t K,
+               size_t gs, int mode, void *ws, size_t wsb, hipStream_t st, float **argmax_pv,
+               int32_t **argmax_pi, int *argmax_np) {
+    size_t Nmax = 0;
+    for (int i = 0; i < nseg; ++i) {
+        int rc = check_common(A, W[i], S[i], M, Ns[i], K, gs);
+        if (rc) return rc;
+        if (Ns[i] > Nmax) Nmax = Ns[i];
+    }
+    if (M == 0 || Nmax == 0) return Q3VL_OK;
+    if (K == 0) {
+        for (int i = 0; i < nseg; ++i)
+            if (C[i]) Q3VL_HIP(hipMemsetAsync(C[i], 0, M * Ns[i] * 4, st), "hipMemsetAsync(C)");
+        return Q3VL_OK;
+    }
+    const WsLayout L = layout(M, Nmax, K, gs);
+    char *wbase = nullptr;
+    int rc = resolve_ws(ws, wsb, L.total, &wbase);
+    if (rc) return rc;
+
+    if (gemv_path_ok(M, K, gs)) {
+        // Lane numerics apply per segment shape; segments sharing one launch
+        // must agree on the path.
+        const bool lanes = q3vl_uses_lane_path(M, Ns[0], K);
+        for (int i = 1; i < nseg; ++i)
+            if (q3vl_uses_lane_path(M, Ns[i], K) != (int)lanes) {
+                for (int j = 0; j < nseg; ++j) {
+                    rc = run_linear(A, 1, &W[j], &S[j], &C[j], &G[j], &Ns[j], M, K, gs,
+                                    GEMV_PLAIN, ws, wsb, st, nullptr, nullptr, nullptr);
+                    if (rc) return rc;
+                }
+                return Q3VL_OK;
+            }
+        if (lanes && K < 1024) return fail(Q3VL_ERR_INVALID_ARGUMENT, "internal: lane path K");
+        GemvArgs a{};
+        a.A = A;
+        a.nseg = nseg;
+        for (int i = 0; i < nseg; ++i) a.seg[i] = {W[i], S[i], C[i], G ? G[i] : nullptr, (int)Ns[i]};
+        a.M = (int)M;
+        a.K = (int)K;
+        a.gs = (int)gs;
+        a.mode = mode;
+        a.part_val = reinterpret_cast<float *>(wbase + L.parts_val);
+        a.part_idx = reinterpret_cast<int32_t *>(wbase + L.parts_idx);
+        int grid = 0;
+        Q3VL_HIP(launch_gemv(a, lanes, &grid, st), "gemv launch");
+        if (argmax_pv) {
+            *argmax_pv = a.part_val;
+            *argmax_pi = a.part_idx;
+            *argmax_np = grid;
+        }
+        return Q3VL_OK;
+    }
+
+    if (M <= 8 && q3vl_uses_lane_path(M, Nmax, K))
+        return fail(Q3VL_ERR_UNSUPPORTED,
+                    "M=1 lane-ordered GEMV needs K <= 8192 (K=%zu, group_size=%zu)", K, gs);
+    if (!gs_ok_gemm(gs) || K % 64 != 0)
+        return fail(Q3VL_ERR_UNSUPPORTED,
+                    "GEMM path needs group_size in {32,64,128} and K %% 64 == 0 "
+                    "(M=%zu K=%zu group_size=%zu)", M, K, gs);
+    // M > 8 (or an M <= 8 shape the GEMV kernels do not take): quantize once.
+    const WsLayout LG = layout(M > 8 ? M : 9, Nmax, K, gs);
+    if (LG.total > L.total) {
+        rc = resolve_ws(ws, wsb, LG.total, &wbase);
+        if (rc) return rc;
+    }
+    _Float16 *aq = reinterpret_cast<_Float16 *>(wbase + LG.aq);
+    float *asT = reinterpret_cast<float *>(wbase + LG.as);
+    Q3VL_HIP(launch_quantize_f16(A, aq, asT, (int)M, (int)K, (int)gs, (int)K, LG.lda_s, st),
+             "quantize launch");
+    if (mode == GEMV_SWIGLU) {
+        GemmArgs g{aq, asT, (int)K, LG.lda_s, W[0], S[0], W[1], S[1], C[0], nullptr,
+                   (int)M, (int)Ns[0], (int)K, (int)gs, true};
+        Q3VL_HIP(launch_gemm(g, st), "gemm launch");
+        return Q3VL_OK;
+    }
+    for (int i = 0; i < nseg; ++i) {
+        float *Ci = C[i];
+        if (mode == GEMV_ARGMAX && !Ci) Ci = reinterpret_cast<float *>(wbase + LG.logits);
+        GemmArgs g{aq, asT, (int)K, LG.lda_s, W[i], S[i], nullptr, nullptr, Ci,
+                   G ? G[i] : nullptr, (int)M, (int)Ns[i], (int)K, (int)gs, false};
+        Q3VL_HIP(launch_gemm(g, st), "gemm launch");
+        if (mode == GEMV_ARGMAX && argmax_pv) {
+            // Caller finishes with argmax over the logits rows.
+            *argmax_pv = reinterpret_cast<float *>(wbase + LG.parts_val);
+            *argmax_pi = reinterpret_cast<int32_t *>(wbase + LG.parts_idx);
+            *argmax_np = -1;  // signals: logits in Ci
+            Q3VL_HIP(launch_argmax_partials(Ci, (int)M, (int)Ns[i], *argmax_pv, *argmax_pi,
+                                            kGemmArgmaxParts, st),
+                     "argmax launch");
+        }
+    }
+    return Q3VL_OK;
+}
+
+// ---- host-weight registry
+struct RegEntry {
+    void *dW = nullptr;
+    void *dS = nullptr;
+    size_t N = 0, K = 0, gs = 0;
+};
+std::mutex g_reg_mu;
+std::unordered_map<const void *, RegEntry> g_reg;
+
+}  // namespace
+
+extern "C" {
+
+const char *q3vl_last_error(void) { return g_err.c_str(); }
+
+int q3vl_abi_version(void) { return Q3VL_ABI_VERSION; }
+
+size_t q3vl_workspace_bytes(size_t M, size_t N, size_t K, size_t group_size) {
+    // The GEMM-path layout (M >= 9) is a superset of the GEMV-path one, and
+    // an M <= 8 shape may fall back to the GEMM kernels.
+    return layout(M > 9 ? M : 9, N, K, group_size ? group_size : 1).total;
+}
+
+int q3vl_check_dtypes(int ta, int tb, int tb_scale, int tc, int has_bias, int group_quantized,
+                      int b_transpose) {
+    if (ta == Q3VL_DTYPE_FP32 && tc == Q3VL_DTYPE_FP32 && tb == Q3VL_DTYPE_INT8 &&
+        tb_scale == Q3VL_DTYPE_FP32 && !has_bias) {
+        if (!group_quantized)
+            return fail(Q3VL_ERR_UNSUPPORTED,
+                        "DType matmul not supported: row-quantized int8 (group_quantized=0)");
+        if (!b_transpose)
+            return fail(Q3VL_ERR_UNSUPPORTED,
+                        "DType matmul not supported: int8 weights need mat_B_transpose=1");
+        return Q3VL_OK;
+    }
+    return fail(Q3VL_ERR_UNSUPPORTED,
+                "DType matmul not supported: type_a=%d, type_b=%d, type_b_scale=%d, type_c=%d, "
+                "bias=%d, group_quantized=%d",
+                ta, tb, tb_scale, tc, has_bias, group_quantized);
+}
+
+int q3vl_uses_lane_path(size_t M, size_t N, size_t K) {
+    return M == 1 && N >= 1024 && K >= 1024;
+}
+
+int q3vl_quantize_rows(const float *A, int16_t *q, float *a_s, size_t M, size_t K,
+                       size_t group_size, q3vl_stream stream) {
+    if (!gs_ok_gemv(group_size) || K % group_size != 0)
+        return fail(Q3VL_ERR_UNSUPPORTED, "group_size=%zu / K=%zu not supported", group_size, K);
+    if (M == 0 || K == 0) return Q3VL_OK;
+    if (!A || !q || !a_s) return fail(Q3VL_ERR_INVALID_ARGUMENT, "null pointer");
+    if (M > 65535) return fail(Q3VL_ERR_UNSUPPORTED, "M=%zu > 65535", M);
+    Q3VL_HIP(launch_quantize_i16(A, q, a_s, (int)M, (int)K, (int)group_size,
+                                 (hipStream_t)stream),
+             "quantize launch");
+    return Q3VL_OK;
+}
+
+int q3vl_linear_i8(const float *A, const int8_t *W, const float *S, float *C, size_t M,
+                   size_t N, size_t K, size_t group_size, void *workspace,
+                   size_t workspace_bytes, q3vl_stream stream) {
+    if (!C && M && N) return fail(Q3VL_ERR_INVALID_ARGUMENT, "null C");
+    int32_t *G = nullptr;
+    return run_linear(A, 1, &W, &S, &C, &G, &N, M, K, group_size, GEMV_PLAIN, workspace,
+                      workspace_bytes, (hipStream_t)stream, nullptr, nullptr, nullptr);
+}
+
+int q3vl_linear_i8_groups(const float *A, const int8_t *W, const float *S, float *C,
+                          int32_t *G, size_t M, size_t N, size_t K, size_t group_size,
+                          void *workspace, size_t workspace_bytes, q3vl_stream stream) {
+    if ((!C || !G) && M && N) return fail(Q3VL_ERR_INVALID_ARGUMENT, "null C or G");
+    return run_linear(A, 1, &W, &S, &C, &G, &N, M, K, group_size, GEMV_PLAIN, workspace,
+                      workspace_bytes, (hipStream_t)stream, nullptr, nullptr, nullptr);
+}
+
+int q3vl_linear_i8_multi(const float *A, size_t M, size_t K, size_t group_size, int count,
+                         const int8_t *const *W, const float *const *S, float *const *C,
+                         const size_t *N, void *workspace, size_t workspace_bytes,
+                         q3vl_stream stream) {
+    if (count < 1 || count > 3 || !W || !S || !C || !N)
+        return fail(Q3VL_ERR_INVALID_ARGUMENT, "count must be 1..3 with non-null arrays");
+    for (int i = 0; i < count; ++i)
+        if (!C[i] && M && N[i]) return fail(Q3VL_ERR_INVALID_ARGUMENT, "null C[%d]", i);
+    int32_t *G[3] = {nullptr, nullptr, nullptr};
+    return run_linear(A, count, W, S, C, G, N, M, K, group_size, GEMV_PLAIN, workspace,
+                      workspace_bytes, (hipStream_t)stream, nullptr, nullptr, nullptr);
+}
+
+int q3vl_linear_i8_swiglu(const float *A, const int8_t *Wg, const float *Sg, const int8_t *Wu,
+                          const float *Su, float *H, size_t M, size_t N, size_t K,
+                          size_t group_size, void *workspace, size_t workspace_bytes,
+                          q3vl_stream stream) {
+    if (!H && M && N) return fail(Q3VL_ERR_INVALID_ARGUMENT, "null H");
+    const int8_t *W[2] = {Wg, Wu};
+    const float *S[2] = {Sg, Su};
+    float *C[2] = {H, nullptr};
+    int32_t *G[2] = {nullptr, nullptr};
+    const size_t Ns[2] = {N, N};
+    return run_linear(A, 2, W, S, C, G, Ns, M, K, group_size, GEMV_SWIGLU, workspace,
+                      workspace_bytes, (hipStream_t)stream, nullptr, nullptr, nullptr);
+}
+
+int q3vl_lm_head_argmax(const float *A, const int8_t *W, const float *S, float *logits,
+                        int32_t *ids, size_t M, size_t V, size_t K, size_t group_size,
+                        void *workspace, size_t workspace_bytes, q3vl_stream stream) {
+    if (!ids && M) return fail(Q3VL_ERR_INVALID_ARGUMENT, "null ids");
+    if (M == 0) return Q3VL_OK;
+    if (V == 0 || V > 0x7fffffff)
+        return fail(Q3VL_ERR_INVALID_ARGUMENT, "vocabulary size V=%zu", V);
+    hipStream_t st = (hipStream_t)stream;
+    float *pv = nullptr;
+    int32_t *pi = nullptr;
+    int np = 0;
+    int32_t *G = nullptr;
+    int rc = run_linear(A, 1, &W, &S, &logits, &G, &V, M, K, group_size, GEMV_ARGMAX, workspace,
+                        workspace_bytes, st, &pv, &pi, &np);
+    if (rc) return rc;
+    if (np == -1) np = kGemmArgmaxParts;  // GEMM path: partials made from the logits
+    if (!pv || np < 1) return fail(Q3VL_ERR_INVALID_ARGUMENT, "argmax: K=0 not supported");
+    Q3VL_HIP(launch_argmax_final(pv, pi, np, (int)M, ids, st), "argmax final launch");
+    return Q3VL_OK;
+}
+
+int q3vl_argmax_rows(const float *logits, int32_t *ids, size_t M, size_t V, void *workspace,
+                     size_t workspace_bytes, q3vl_stream stream) {
+    if (M == 0) return Q3VL_OK;
+    if (!logits || !ids) return fail(Q3VL_ERR_INVALID_ARGUMENT, "null pointer");
+    if (V == 0 || V > 0x7fffffff || M > 65535)
+        return fail(Q3VL_ERR_INVALID_ARGUMENT, "bad shape M=%zu V=%zu", M, V);
+    const int nparts = 64;
+    const size_t need = 2 * align256((size_t)nparts * M * 4);
+    char *w = nullptr;
+    int rc = resolve_ws(workspace, workspace_bytes, need, &w);
+    if (rc) return rc;
+    float *pv = reinterpret_cast<float *>(w);
+    int32_t *pi = reinterpret_cast<int32_t *>(w + align256((size_t)nparts * M * 4));
+    Q3VL_HIP(launch_argmax_rows(logits, (int)M, (int)V, pv, pi, nparts, ids,
+                                (hipStream_t)stream),
+             "argmax launch");
+    return Q3VL_OK;
+}
+
+int q3vl_swiglu(float *gate, const float *up, size_t n, q3vl_stream stream) {
+    if (n == 0) return Q3VL_OK;
+    if (!gate || !up) return fail(Q3VL_ERR_INVALID_ARGUMENT, "null pointer");
+    Q3VL_HIP(launch_swiglu(gate, up, n, (hipStream_t)stream), "swiglu launch");
+    return Q3VL_OK;
+}
+
+int q3vl_weight_register(const int8_t *host_W, const float *host_S, size_t N, size_t K,
+                         size_t group_size, const int8_t **dev_W, const float **dev_S) {
+    if (!host_W || !host_S || !group_size || K % group_size)
+        return fail(Q3VL_ERR_INVALID_ARGUMENT, "bad weight registration arguments");
+    std::lock_guard<std::mutex> lk(g_reg_mu);
+    auto it = g_reg.find(host_W);
+    if (it != g_reg.end()) {
+        const RegEntry &e = it->second;
+        if (e.N != N || e.K != K || e.gs != group_size)
+            return fail(Q3VL_ERR_INVALID_ARGUMENT,
+                        "host weight %p already registered with another shape", (const void *)host_W);
+    } else {
+        RegEntry e;
+        e.N = N;
+        e.K = K;
+        e.gs = group_size;
+        const size_t wb = N * K, sb = N * (K / group_size) * 4;
+        if (hipMalloc(&e.dW, wb ? wb : 1) != hipSuccess ||
+            hipMalloc(&e.dS, sb ? sb : 1) != hipSuccess) {
+            if (e.dW) (void)hipFree(e.dW);
+            return fail(Q3VL_ERR_OUT_OF_MEMORY, "weight upload: hipMalloc failed");
+        }
+        hipError_t err = hipMemcpy(e.dW, host_W, wb, hipMemcpyHostToDevice);
+        if (err == hipSuccess) err = hipMemcpy(e.dS, host_S, sb, hipMemcpyHostToDevice);
+        if (err != hipSuccess) {
+            (void)hipFree(e.dW);
+            (void)hipFree(e.dS);
+            return hip_fail(err, "weight upload");
+        }
+        it = g_reg.emplace(host_W, e).first;
+    }
+    if (dev_W) *dev_W = static_cast<const int8_t *>(it->second.dW);
+    if (dev_S) *dev_S = static_cast<const float *>(it->second.dS);
+    return Q3VL_OK;
+}
+
+int q3vl_weight_lookup(const void *host_W, const int8_t **dev_W, const float **dev_S) {
+    std::lock_guard<std::mutex> lk(g_reg_mu);
+    auto it = g_reg.find(host_W);
+    if (it == g_reg.end())
+        return fail(Q3VL_ERR_INVALID_ARGUMENT, "host weight %p is not registered", host_W);
+    if (dev_W) *dev_W = static_cast<const int8_t *>(it->second.dW);
+    if (dev_S) *dev_S = static_cast<const float *>(it->second.dS);
+    return Q3VL_OK;
+}
+
+int q3vl_weight_release(const void *host_W) {
+    std::lock_guard<std::mutex> lk(g_reg_mu);
+    auto it = g_reg.find(host_W);
+    if (it == g_reg.end())
+        return fail(Q3VL_ERR_INVALID_ARGUMENT, "host weight %p is not registered", host_W);
+    Q3VL_HIP(hipDeviceSynchronize(), "hipDeviceSynchronize");
+    (void)hipFree(it->second.dW);
+    (void)hipFree(it->second.dS);
+    g_reg.erase(it);
+    return Q3VL_OK;
+}
+
+int q3vl_weight_release_all(void) {
+    std::lock_guard<std::mutex> lk(g_reg_mu);
+    if (!g_reg.empty()) Q3VL_HIP(hipDeviceSynchronize(), "hipDeviceSynchronize");
+    for (auto &kv : g_reg) {
+        (void)hipFree(kv.second.dW);
+        (void)hipFree(kv.second.dS);
+    }
+    g_reg.clear();
+    return Q3VL_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,312 @@
+// gemm.hip -- int8-weight GEMM for M > 8 on gfx950 matrix cores.
+//
+// Reference: the general path of linear_int8_fp32s_int32acc_transpose,
+// matmul/src/cpu_f32a_i8f32sb_f32c_avx2.cpp:477-662: per output and per
+// K-group g (ascending), G = sum_k q[m,k] * w[n,k] exactly in int32, then
+//     acc = fma(float(G) * a_s[m,g], w_s[n,g], acc)          (:613-617, 652)
+// (GCC contracts the multiply-add; the golden vectors pin this).
+//
+// Exactness on MFMA. q is int16 with |q| <= 1016, so q and w are exact in
+// fp16; every partial sum of one group is an integer below 2^24 in magnitude,
+// so v_mfma_f32_32x32x16_f16 accumulating one group in fp32 yields G exactly.
+// The accumulator is consumed and cleared at every group boundary by the fp32
+// epilogue above, in group order, so C is bit-identical to the reference.
+//
+// Tiling: block 128(M) x 128(N) x 64(K), 4 waves in 2x2, each wave 64x64 =
+// 2x2 MFMA 32x32 tiles. A (fp16) and B (int8) tiles are staged through LDS
+// (double buffered, XOR-swizzled 16-byte slots); B is widened to fp16 in
+// registers with the 0x64xx exponent trick: half(0x6400|(b^0x80)) - 1152 = b.
+// In SwiGLU mode the block's 128 B rows are 64 gate rows and the same 64 up
+// rows, and each wave holds a gate tile and the matching up tile so the
+// epilogue silu(g)*u needs no exchange.
+#include "q3vl_device.hpp"
+#include "q3vl_kernels.hpp"
+
+namespace q3vl {
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef float float16_t __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int BM = 128, BN = 128, BK = 64;
+constexpr int A_STAGE = BM * BK * 2;  // bytes
+constexpr int B_STAGE = BN * BK;      // bytes
+constexpr int SC_STAGE = 2 * (BM + BN) * 4;  // up to 2 groups of a_s and w_s
+
+__device__ __forceinline__ float silu_mul_g(float gv, float uv) {
+    const float e = (float)::exp(-(double)gv);
+    const float den = 1.0f + e;
+    const float sl = (float)((double)gv / (double)den);
+    return sl * uv;
+}
+
+// 4 bytes (already xor 0x80) -> 4 fp16 values in two dwords.
+__device__ __forceinline__ void widen4(uint32_t x, uint32_t &lo, uint32_t &hi) {
+    const uint32_t e = 0x64646464u;
+    const uint32_t l = __builtin_amdgcn_perm(e, x, 0x04010400u);
+    const uint32_t h = __builtin_amdgcn_perm(e, x, 0x04030402u);
+    const half2_t off = {(_Float16)1152.0f, (_Float16)1152.0f};
+    lo = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, l) - off);
+    hi = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, h) - off);
+}
+
+template <bool SWIGLU, bool WITH_G>
+__global__ __launch_bounds__(256, 2) void gemm_i8_kernel(GemmArgs a) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    auto As = [&](int b) { return smem + b * A_STAGE; };
+    auto Bs = [&](int b) { return smem + 2 * A_STAGE + b * B_STAGE; };
+    auto Sc = [&](int b) {
+        return reinterpret_cast<float *>(smem + 2 * A_STAGE + 2 * B_STAGE + b * SC_STAGE);
+    };
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wid = tid >> 6;
+    const int wm = wid & 1, wn = wid >> 1;
+    const int l32 = lane & 31, h = lane >> 5;
+
+    const int M = a.M, N = a.N, K = a.K, gs = a.gs;
+    const int Kg = K / gs;
+    const int m0 = blockIdx.y * BM;
+    const int nb = SWIGLU ? BN / 2 : BN;  // output columns per block
+    const int n0 = blockIdx.x * nb;
+    const int nkb = K / BK;
+    const int gpb = gs < BK ? BK / gs : 1;  // groups inside one BK slice
+
+    // ---- staging assignment
+    // A: 1024 16-byte chunks (row = c/8, slot = c%8), 4 per thread.
+    // B: 512 chunks (row = c/4, slot = c%4), 2 per thread.
+    // Row r of the A stage holds activation row m0 + r; chunk c of thread
+    // tid + 256 i is (row c/8, 16-byte slot c%8). Offsets are element offsets
+    // at k = 0 (32-bit: M*lda and N*K stay below 2^31 by the host checks).
+    uint32_t a_off[4];
+    int a_dst[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int c = tid + 256 * i;
+        const int row = c >> 3, slot = c & 7;
+        const int mrow = min(m0 + row, M - 1);
+        a_off[i] = (uint32_t)mrow * (uint32_t)a.lda + slot * 8;
+        a_dst[i] = row * 128 + ((slot ^ ((row >> 1) & 7)) << 4);
+    }
+    // B: row c/4 of the stage, slot c%4. With SWIGLU, stage rows 64..127 are
+    // the up rows (thread chunks i=1 cover rows 64..127 exactly).
+    uint32_t b_off[2];
+    int b_dst[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int c = tid + 256 * i;
+        const int row = c >> 2, slot = c & 3;
+        const int nrow = min(n0 + (SWIGLU ? (row & 63) : row), N - 1);
+        b_off[i] = (uint32_t)nrow * (uint32_t)K + slot * 16;
+        b_dst[i] = row * 64 + ((slot ^ ((row >> 2) & 3)) << 4);
+    }
+    // scales: thread t < 2*(BM+BN) loads one value per stage
+    //   [0, BM*gpb): a_s of group j = t / BM, row t % BM
+    //   [2*BM, 2*BM + BN*gpb): w_s of group j, column (t-2BM) % BN
+    const int sc_i = tid;  // 256 threads cover 2*(128+128)=512 slots in 2 passes
+
+    u32x4 ra[4], rb[2];
+    float rs[2];
+
+    auto load_regs = [&](int kb) {
+        const int k0 = kb * BK;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ra[i] = *reinterpret_cast<const u32x4 *>(a.Aq + a_off[i] + k0);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int8_t *W = (SWIGLU && i == 1) ? a.W1 : a.W0;
+            rb[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(W + b_off[i] + k0));
+        }
+        const int g0 = k0 / gs;
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+            const int s = sc_i + 256 * p;
+            float v = 0.0f;
+            if (s < 2 * BM) {
+                const int j = s / BM, r = s % BM;
+                if (j < gpb) v = a.a_s[(size_t)(g0 + j) * a.lda_s + min(m0 + r, M - 1)];
+            } else {
+                const int t = s - 2 * BM;
+                const int j = t / BN, c = t % BN;
+                if (j < gpb) {
+                    const float *S;
+                    int nrow;
+                    if (SWIGLU) {
+                        S = c < 64 ? a.S0 : a.S1;
+                        nrow = n0 + (c & 63);
+                    } else {
+                        S = a.S0;
+                        nrow = n0 + c;
+                    }
+                    nrow = min(nrow, N - 1);
+                    v = S[(size_t)nrow * Kg + g0 + j];
+                }
+            }
+            rs[p] = v;
+        }
+    };
+    auto store_lds = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4 *>(As(buf) + a_dst[i]) = ra[i];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            u32x4 v = rb[i];
+            v ^= (u32x4){0x80808080u, 0x80808080u, 0x80808080u, 0x80808080u};
+            *reinterpret_cast<u32x4 *>(Bs(buf) + b_dst[i]) = v;
+        }
+#pragma unroll
+        for (int p = 0; p < 2; ++p) Sc(buf)[sc_i + 256 * p] = rs[p];
+    };
+
+    float16_t cacc[2][2], out[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            cacc[i][j] = (float16_t)(0.0f);
+            out[i][j] = (float16_t)(0.0f);
+        }
+
+    // B row (inside the block tile) of this lane's column for n-tile nt
+    int brow[2];
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt)
+        brow[nt] = SWIGLU ? (nt * 64 + wn * 32 + l32) : (wn * 64 + nt * 32 + l32);
+    int arow[2];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) arow[mt] = wm * 64 + mt * 32 + l32;
+
+    load_regs(0);
+    store_lds(0);
+    __syncthreads();
+
+    for (int kb = 0; kb < nkb; ++kb) {
+        const int buf = kb & 1;
+        if (kb + 1 < nkb) load_regs(kb + 1);
+
+#pragma unroll
+        for (int sp = 0; sp < 2; ++sp) {
+            // A fragments: row arow[mt], halves [32sp + 16h, +16) = slots 4sp+2h, +1
+            half8_t af[2][2];
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt) {
+                const int r = arow[mt];
+                const int sw = (r >> 1) & 7;
+                const int s0 = 4 * sp + 2 * h;
+                af[mt][0] = *reinterpret_cast<const half8_t *>(As(buf) + r * 128 + ((s0 ^ sw) << 4));
+                af[mt][1] =
+                    *reinterpret_cast<const half8_t *>(As(buf) + r * 128 + (((s0 + 1) ^ sw) << 4));
+            }
+            // B fragments: row brow[nt], bytes [32sp + 16h, +16) = slot 2sp+h
+            half8_t bf[2][2];
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) {
+                const int r = brow[nt];
+                const int slot = (2 * sp + h) ^ ((r >> 2) & 3);
+                const u32x4 raw = *reinterpret_cast<const u32x4 *>(Bs(buf) + r * 64 + (slot << 4));
+                uint32_t w[8];
+                widen4(raw.x, w[0], w[1]);
+                widen4(raw.y, w[2], w[3]);
+                widen4(raw.z, w[4], w[5]);
+                widen4(raw.w, w[6], w[7]);
+                bf[nt][0] = __builtin_bit_cast(half8_t, (u32x4){w[0], w[1], w[2], w[3]});
+                bf[nt][1] = __builtin_bit_cast(half8_t, (u32x4){w[4], w[5], w[6], w[7]});
+            }
+#pragma unroll
+            for (int u = 0; u < 2; ++u)
+#pragma unroll
+                for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+                    for (int nt = 0; nt < 2; ++nt)
+                        cacc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                            af[mt][u], bf[nt][u], cacc[mt][nt], 0, 0, 0);
+
+            // ---- group boundary: fp32 epilogue in reference order
+            const int kend = kb * BK + 32 * sp + 32;  // K consumed so far
+            if (kend % gs == 0) {
+                const int g = kend / gs - 1;
+                const int j = g - (kb * BK) / gs;  // group slot inside this stage
+                const float *asT = Sc(buf) + j * BM;
+                const float *wsT = Sc(buf) + 2 * BM + j * BN;
+#pragma unroll
+                for (int mt = 0; mt < 2; ++mt) {
+                    float asv[16];
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const float4 v = *reinterpret_cast<const float4 *>(
+                            asT + wm * 64 + mt * 32 + 8 * q + 4 * h);
+                        asv[4 * q + 0] = v.x;
+                        asv[4 * q + 1] = v.y;
+                        asv[4 * q + 2] = v.z;
+                        asv[4 * q + 3] = v.w;
+                    }
+#pragma unroll
+                    for (int nt = 0; nt < 2; ++nt) {
+                        const float wsv = wsT[brow[nt]];
+#pragma unroll
+                        for (int e = 0; e < 16; ++e) {
+                            const float t = cacc[mt][nt][e] * asv[e];
+                            out[mt][nt][e] = fmaf(t, wsv, out[mt][nt][e]);
+                        }
+                        if (WITH_G) {
+                            const int ncol = n0 + brow[nt];
+                            if (ncol < N) {
+#pragma unroll
+                                for (int e = 0; e < 16; ++e) {
+                                    const int mrow =
+                                        m0 + wm * 64 + mt * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
+                                    if (mrow < M)
+                                        a.G[((size_t)mrow * N + ncol) * Kg + g] =
+                                            (int32_t)cacc[mt][nt][e];
+                                }
+                            }
+                        }
+                        cacc[mt][nt] = (float16_t)(0.0f);
+                    }
+                }
+            }
+        }
+
+        if (kb + 1 < nkb) store_lds(buf ^ 1);
+        __syncthreads();
+    }
+
+    // ---- store
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const int mrow = m0 + wm * 64 + mt * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
+            if (mrow >= M) continue;
+            if (SWIGLU) {
+                const int ncol = n0 + wn * 32 + l32;
+                if (ncol < N)
+                    a.C[(size_t)mrow * N + ncol] = silu_mul_g(out[mt][0][e], out[mt][1][e]);
+            } else {
+#pragma unroll
+                for (int nt = 0; nt < 2; ++nt) {
+                    const int ncol = n0 + brow[nt];
+                    if (ncol < N) a.C[(size_t)mrow * N + ncol] = out[mt][nt][e];
+                }
+            }
+        }
+    }
+}
+
+hipError_t launch_gemm(const GemmArgs &a, hipStream_t st) {
+    // gs <= 128 keeps every in-group fp32 partial sum below 2^24 (exact).
+    if (a.K % BK != 0 || (a.gs != 32 && a.gs != 64 && a.gs != 128))
+        return hipErrorInvalidValue;
+    if (a.swiglu && a.G) return hipErrorInvalidValue;
+    const int nb = a.swiglu ? BN / 2 : BN;
+    dim3 grid((a.N + nb - 1) / nb, (a.M + BM - 1) / BM);
+    const size_t lds = 2 * (A_STAGE + B_STAGE + SC_STAGE);
+    if (a.swiglu) gemm_i8_kernel<true, false><<<grid, 256, lds, st>>>(a);
+    else if (a.G) gemm_i8_kernel<false, true><<<grid, 256, lds, st>>>(a);
+    else gemm_i8_kernel<false, false><<<grid, 256, lds, st>>>(a);
+    return hipGetLastError();
+}
+
+}  // namespace q3vl

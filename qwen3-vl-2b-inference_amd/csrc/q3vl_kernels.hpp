@@ -1,0 +1,80 @@
+// q3vl_kernels.hpp -- host-side launchers of the gfx950 kernels (internal to
+// libq3vl_int8.so; the public surface is include/q3vl_int8.h).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace q3vl {
+
+// ---------------------------------------------------------------- quantizer
+hipError_t launch_quantize_i16(const float *A, int16_t *q, float *a_s, int M, int K,
+                               int gs, hipStream_t st);
+// fp16 images of q (exact: |q| <= 1016) with row stride ldq, and a_s stored
+// transposed as a_sT[g * lda_s + m] for the GEMM epilogue.
+hipError_t launch_quantize_f16(const float *A, _Float16 *q, float *a_sT, int M, int K,
+                               int gs, int ldq, int lda_s, hipStream_t st);
+
+// ------------------------------------------------------------ GEMV (M <= 8)
+// Up to three weight matrices stacked along N share one quantized activation.
+struct GemvSeg {
+    const int8_t *W;  // [N, K] int8, reference layout (mat_B_transpose=true)
+    const float *S;   // [N, K/gs] fp32 group scales
+    float *Y;         // [M, N] fp32 output (row stride N)
+    int32_t *G;       // optional [M, N, K/gs] int32 group sums (debug), or null
+    int N;
+};
+
+enum GemvMode : int {
+    GEMV_PLAIN = 0,   // Y_s = A W_s^T for every segment
+    GEMV_SWIGLU = 1,  // seg0 = gate, seg1 = up: seg0.Y = silu(gate) * up
+    GEMV_ARGMAX = 2,  // seg0 only: per-row argmax partials (+ logits if Y)
+};
+
+struct GemvArgs {
+    const float *A;   // [M, K] fp32 activations
+    GemvSeg seg[3];
+    int nseg;
+    int M, K, gs;
+    int mode;
+    float *part_val;  // GEMV_ARGMAX: [grid, M] block partial maxima
+    int32_t *part_idx;  // [grid, M] block partial indices (-1: none)
+};
+
+// lanes=true: the reference's M=1 path (i8:122-224 / 327-455) -- per-lane
+// fp32 FMA chains and the fixed 8-lane tree. lanes=false: the general path
+// (i8:477-662) -- acc = fma(G*a_s, w_s, acc), M <= 8.
+// Returns the grid size used (argmax partial count) through *grid_out.
+hipError_t launch_gemv(const GemvArgs &a, bool lanes, int *grid_out, hipStream_t st);
+
+// Final argmax over block partials: ids[m] = first index of the maximum.
+hipError_t launch_argmax_final(const float *part_val, const int32_t *part_idx,
+                               int nparts, int M, int32_t *ids, hipStream_t st);
+// Block partials of greedy argmax over rows of logits ([nparts, M] layout).
+hipError_t launch_argmax_partials(const float *logits, int M, int V, float *part_val,
+                                  int32_t *part_idx, int nparts, hipStream_t st);
+// Stand-alone greedy argmax over rows of logits (partials + final).
+hipError_t launch_argmax_rows(const float *logits, int M, int V, float *part_val,
+                              int32_t *part_idx, int nparts, int32_t *ids,
+                              hipStream_t st);
+// Stand-alone swiglu: gate[i] = silu(gate[i]) * up[i].
+hipError_t launch_swiglu(float *gate, const float *up, size_t n, hipStream_t st);
+
+// ---------------------------------------------------------- GEMM (MFMA)
+struct GemmArgs {
+    const _Float16 *Aq;  // [M, lda] exact fp16 images of the int16 activations
+    const float *a_s;    // transposed: a_s[g * lda_s + m]
+    int lda;
+    int lda_s;
+    const int8_t *W0;    // [N, K] (gate when swiglu)
+    const float *S0;
+    const int8_t *W1;    // up weights when swiglu, else null
+    const float *S1;
+    float *C;            // [M, N] output (H when swiglu)
+    int32_t *G;          // optional [M, N, K/gs] group sums (not with swiglu)
+    int M, N, K, gs;
+    bool swiglu;
+};
+hipError_t launch_gemm(const GemmArgs &a, hipStream_t st);
+
+}  // namespace q3vl

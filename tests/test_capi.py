@@ -1,0 +1,58 @@
+"""C ABI checks that need no GPU: the libraries load, export every function
+include/q3vl_int8.h declares, and the host-only dispatch logic follows the
+reference's linear() acceptance rules (matmul/src/cpu_wrapper.cpp:320-395)."""
+import ctypes
+import subprocess
+
+import pytest
+
+import q3vl_int8 as q
+
+
+def test_library_exports_every_declared_function():
+    lib = q.lib()
+    names = q.header_functions()
+    assert len(names) >= 15
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+    assert lib.q3vl_abi_version() == 1
+
+
+def test_linear_dropin_exports_cpp_linear():
+    out = subprocess.run(["nm", "-DC", q.LINEAR_LIB_PATH], capture_output=True, text=True,
+                         check=True).stdout
+    assert "T linear(void const*, void const*, void const*, void const*, void const*, void*," in out
+    ctypes.CDLL(q.LINEAR_LIB_PATH)  # loads (resolves libq3vl_int8.so via rpath)
+
+
+@pytest.mark.parametrize("combo,ok", [
+    ((q.FP32, q.INT8, q.FP32, q.FP32, 0, 1, 1), True),
+    ((q.FP32, q.INT8, q.FP32, q.FP32, 1, 1, 1), False),   # bias rejected (:339)
+    ((q.FP32, q.INT8, q.FP32, q.FP32, 0, 0, 1), False),   # row-quantized path
+    ((q.FP32, q.INT8, q.FP32, q.FP32, 0, 1, 0), False),   # non-transposed B
+    ((q.FP16, q.INT8, q.FP32, q.FP32, 0, 1, 1), False),
+    ((q.FP32, q.FP16, q.FP32, q.FP32, 0, 1, 1), False),   # fp16 weights: not this path
+    ((q.FP32, q.INT8, q.FP16, q.FP32, 0, 1, 1), False),
+    ((q.FP32, q.INT8, q.FP32, q.FP16, 0, 1, 1), False),
+])
+def test_dtype_acceptance(combo, ok):
+    rc = q.check_dtypes(*combo)
+    assert (rc == q.OK) == ok
+    if not ok:
+        assert rc == q.ERR_UNSUPPORTED
+        assert "not supported" in q.last_error()
+
+
+def test_lane_path_rule():
+    assert q.uses_lane_path(1, 1024, 1024)
+    assert q.uses_lane_path(1, 151936, 2048)
+    assert not q.uses_lane_path(1, 1000, 2048)
+    assert not q.uses_lane_path(1, 2048, 512)
+    assert not q.uses_lane_path(8, 151936, 2048)
+
+
+def test_workspace_bytes_covers_shapes():
+    small = q.workspace_bytes(1, 6144, 2048, 64)
+    big = q.workspace_bytes(512, 12288, 2048, 64)
+    assert 0 < small < big
+    assert big >= 512 * 2048 * 2 + 512 * 32 * 4

@@ -1,0 +1,278 @@
+"""GPU parity: the HIP library (through its C ABI) against the CPU oracle on the
+same seeded inputs. Integer results (q, group sums, argmax ids) and the fp32
+outputs of every linear are compared bit for bit; SwiGLU outputs, which go
+through expf, are allowed 1 ulp (tolerance stated per test)."""
+import ctypes
+
+import numpy as np
+import pytest
+
+from golden.gen import make_case, tie_group_row
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+import q3vl_int8 as q  # noqa: E402
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+def assert_bits_equal(got, want, what=""):
+    g, w = bits(got), bits(want)
+    bad = np.flatnonzero(g.ravel() != w.ravel())
+    assert bad.size == 0, f"{what}: {bad.size} of {g.size} differ, first at {bad[:5]}: " \
+        f"{got.ravel()[bad[:5]]} vs {want.ravel()[bad[:5]]}"
+
+
+def ulp_diff(a, b):
+    ia = bits(a).astype(np.int64)
+    ib = bits(b).astype(np.int64)
+    ia = np.where(ia >= 2**31, 2**31 - ia, ia)
+    ib = np.where(ib >= 2**31, 2**31 - ib, ib)
+    return np.abs(ia - ib)
+
+
+def test_library_is_native():
+    assert q.lib()._name == q.LIB_PATH
+    assert torch.cuda.is_available()
+
+
+# ------------------------------------------------------------------ quantizer
+@pytest.mark.parametrize("M,K,gs", [(1, 2048, 64), (4, 1024, 16), (3, 2048, 32), (2, 2048, 128),
+                                    (2, 4096, 256), (512, 2048, 64), (7, 6144, 64)])
+def test_quantize_parity(orc, M, K, gs):
+    rng = np.random.default_rng(M * 1000 + gs)
+    A = (rng.standard_normal((M, K)) * rng.uniform(0.01, 50, (M, 1))).astype(np.float32)
+    A[0, :gs] = 0.0                      # zero group
+    if K >= 3 * gs:
+        A[0, gs:2 * gs] = 0.3            # constant group
+        A[0, 2 * gs:3 * gs] = 0.0
+        A[0, 2 * gs + 5] = 7.0           # spike group
+    qq, ss = q.quantize_rows(dev(A), gs)
+    q_ref, s_ref = orc.quantize_rows(A, gs)
+    np.testing.assert_array_equal(host(qq), q_ref)
+    assert_bits_equal(host(ss), s_ref, "a_s")
+
+
+def test_quantize_ties_round_half_even(orc):
+    row = tie_group_row(orc)
+    qq, ss = q.quantize_rows(dev(row), 64)
+    q_ref, s_ref = orc.quantize_rows(row, 64)
+    assert s_ref[0, 0] == 1.0
+    np.testing.assert_array_equal(host(qq), q_ref)
+
+
+# --------------------------------------------------------------- linear paths
+LANE = [(1, 1024, 1024, 64), (1, 6144, 2048, 64), (1, 2048, 6144, 64), (1, 4096, 2048, 64),
+        (1, 1024, 2048, 16), (1, 1024, 2048, 32), (1, 1024, 2048, 128), (1, 1024, 4096, 256),
+        (1, 1028, 1024, 64), (1, 1031, 1024, 64), (1, 70000, 1024, 64)]
+GENERAL = [(1, 512, 2048, 64), (1, 2048, 512, 64), (2, 256, 512, 64), (3, 1000, 2048, 64),
+           (5, 1028, 1024, 32), (8, 1000, 2048, 64), (8, 384, 6144, 64), (4, 77, 1024, 128),
+           (6, 96, 256, 16), (2, 64, 1024, 256)]
+GEMM = [(9, 128, 1024, 64), (16, 384, 1024, 64), (64, 512, 2048, 64), (196, 320, 4096, 64),
+        (130, 200, 1024, 32), (100, 260, 2048, 128), (512, 2048, 6144, 64)]
+
+
+def run_linear_case(orc, M, N, K, gs, seed, groups):
+    A, W, S = make_case(seed, M, N, K, gs)
+    dA, dW, dS = dev(A), dev(W), dev(S)
+    G = torch.zeros((M, N, K // gs), dtype=torch.int32, device="cuda") if groups else None
+    C = q.linear_i8(dA, dW, dS, gs, groups=G)
+    C_ref, G_ref = orc.linear(A, W, S, gs, groups=True)
+    assert_bits_equal(host(C), C_ref, f"C {M}x{N}x{K} gs{gs}")
+    if groups:
+        np.testing.assert_array_equal(host(G), G_ref)
+
+
+@pytest.mark.parametrize("M,N,K,gs", LANE, ids=[str(c) for c in LANE])
+def test_lane_gemv_parity(orc, M, N, K, gs):
+    assert q.uses_lane_path(M, N, K)
+    run_linear_case(orc, M, N, K, gs, seed=N + K + gs, groups=N <= 8192)
+
+
+@pytest.mark.parametrize("M,N,K,gs", GENERAL, ids=[str(c) for c in GENERAL])
+def test_general_gemv_parity(orc, M, N, K, gs):
+    assert not q.uses_lane_path(M, N, K)
+    run_linear_case(orc, M, N, K, gs, seed=M * 7 + N + K, groups=True)
+
+
+@pytest.mark.parametrize("M,N,K,gs", GEMM, ids=[str(c) for c in GEMM])
+def test_gemm_parity(orc, M, N, K, gs):
+    run_linear_case(orc, M, N, K, gs, seed=M + N + K, groups=M * N * K <= 64 * 512 * 2048)
+
+
+def test_golden_vectors_on_gpu():
+    """The reference's own outputs (golden fixtures) reproduced by the GPU."""
+    import json
+    import os
+    from golden.make_golden import LIN_CASES
+    gdir = os.path.join(os.path.dirname(__file__), "golden")
+    gold = np.load(os.path.join(gdir, "golden_int8.npz"))
+    for name, seed, M, N, K, gs in LIN_CASES:
+        A, W, S = make_case(seed, M, N, K, gs)
+        C = q.linear_i8(dev(A), dev(W), dev(S), gs)
+        assert_bits_equal(host(C), gold[f"lin_{name}_C"], name)
+    for name, M in (("lane", 1), ("general", 2)):
+        A = gold[f"probe_{name}_A"]
+        K = A.shape[1]
+        C = q.linear_i8(dev(A), dev(np.eye(K, dtype=np.int8)), dev(np.ones((K, K // 64), np.float32)), 64)
+        assert_bits_equal(host(C), gold[f"probe_{name}_C"], f"probe {name}")
+
+
+def test_nonfinite_activation_rows_stay_nonfinite(orc):
+    A, W, S = make_case(5, 1, 2048, 2048, 64)
+    A[0, 3] = np.nan
+    C = host(q.linear_i8(dev(A), dev(W), dev(S), 64))
+    C_ref = orc.linear(A, W, S, 64)
+    assert np.array_equal(np.isnan(C), np.isnan(C_ref)) and np.isnan(C).all()
+
+
+# -------------------------------------------------------------- fused consumers
+@pytest.mark.parametrize("M,N,K", [(1, 6144, 2048), (1, 1024, 1024), (4, 512, 1024), (64, 512, 1024),
+                                   (512, 768, 2048)])
+def test_swiglu_fused_parity(orc, M, N, K):
+    gs = 64
+    A, Wg, Sg = make_case(100 + M, M, N, K, gs)
+    _, Wu, Su = make_case(200 + M, M, N, K, gs)
+    H = host(q.linear_i8_swiglu(dev(A), dev(Wg), dev(Sg), dev(Wu), dev(Su), gs))
+    g = orc.linear(A, Wg, Sg, gs)
+    u = orc.linear(A, Wu, Su, gs)
+    H_ref = orc.swiglu(g, u)
+    # tolerance: expf rounding may differ by 1 ulp from libm; everything else exact
+    d = ulp_diff(H, H_ref)
+    assert d.max() <= 2, d.max()
+    assert (d == 0).mean() > 0.999
+
+
+def test_swiglu_standalone(orc):
+    from golden.make_golden import swiglu_inputs
+    g, u = swiglu_inputs()
+    out = host(q.swiglu(dev(g), dev(u)))
+    d = ulp_diff(out, orc.swiglu(g, u))
+    assert d.max() <= 2 and (d == 0).mean() > 0.999
+
+
+@pytest.mark.parametrize("M", [1, 8])
+def test_lm_head_argmax_parity(orc, M):
+    V, K, gs = 151936, 2048, 64
+    A, W, S = make_case(300 + M, M, V, K, gs)
+    # plant exact ties: copy the winning row of activation row 0 to a lower
+    # and a higher index -> the lowest index must win
+    logits_ref = orc.linear(A, W, S, gs)
+    top = int(orc.argmax_rows(logits_ref[:1])[0])
+    W[top + 7] = W[top]
+    S[top + 7] = S[top]
+    lo = max(0, top - 1000)
+    W[lo] = W[top]
+    S[lo] = S[top]
+    logits_ref = orc.linear(A, W, S, gs)
+    ids_ref = orc.argmax_rows(logits_ref)
+    assert ids_ref[0] == lo
+    dW, dS, dA = dev(W), dev(S), dev(A)
+    logits = torch.empty((M, V), dtype=torch.float32, device="cuda")
+    ids = host(q.lm_head_argmax(dA, dW, dS, gs, logits=logits))
+    assert_bits_equal(host(logits), logits_ref, "logits")
+    np.testing.assert_array_equal(ids, ids_ref)
+    ids2 = host(q.lm_head_argmax(dA, dW, dS, gs))  # logits not stored
+    np.testing.assert_array_equal(ids2, ids_ref)
+
+
+def test_lm_head_argmax_gemm_path(orc):
+    M, V, K, gs = 12, 5000, 1024, 64
+    A, W, S = make_case(77, M, V, K, gs)
+    ids = host(q.lm_head_argmax(dev(A), dev(W), dev(S), gs))
+    np.testing.assert_array_equal(ids, orc.argmax_rows(orc.linear(A, W, S, gs)))
+
+
+def test_argmax_rows_special_values(orc):
+    fmax = np.finfo(np.float32).max
+    rows = np.full((6, 3000), -np.inf, np.float32)
+    rows[1, :] = np.nan
+    rows[1, 2000] = 1.0
+    rows[2, :] = -fmax
+    rows[3, 10] = rows[3, 2999] = 5.0
+    rows[4, :] = 0.0
+    rows[4, 0] = -0.0
+    rows[5] = np.random.default_rng(1).integers(-3, 3, 3000).astype(np.float32)
+    ids = host(q.argmax_rows(dev(rows)))
+    np.testing.assert_array_equal(ids, orc.argmax_rows(rows))
+
+
+def test_multi_matches_separate(orc):
+    gs, K = 64, 2048
+    A, Wq, Sq = make_case(1, 1, 2048, K, gs)
+    _, Wk, Sk = make_case(2, 1, 1024, K, gs)
+    _, Wv, Sv = make_case(3, 1, 1024, K, gs)
+    outs = q.linear_i8_multi(dev(A), [dev(Wq), dev(Wk), dev(Wv)], [dev(Sq), dev(Sk), dev(Sv)], gs)
+    for o, (W, S) in zip(outs, [(Wq, Sq), (Wk, Sk), (Wv, Sv)]):
+        assert_bits_equal(host(o), orc.linear(A, W, S, gs), "multi")
+    # mixed paths (N < 1024 segment with M=1) fall back to separate launches
+    _, Ws, Ss = make_case(4, 1, 512, K, gs)
+    outs = q.linear_i8_multi(dev(A), [dev(Wq), dev(Ws)], [dev(Sq), dev(Ss)], gs)
+    assert_bits_equal(host(outs[1]), orc.linear(A, Ws, Ss, gs), "multi mixed")
+
+
+def test_caller_workspace(orc):
+    M, N, K, gs = 64, 256, 1024, 64
+    A, W, S = make_case(8, M, N, K, gs)
+    ws = q.alloc_workspace(M, N, K, gs)
+    C = q.linear_i8(dev(A), dev(W), dev(S), gs, workspace=ws)
+    assert_bits_equal(host(C), orc.linear(A, W, S, gs))
+    with pytest.raises(q.Q3VLError) as e:
+        q.linear_i8(dev(A), dev(W), dev(S), gs, workspace=ws[:1024])
+    assert e.value.code == q.ERR_INVALID_ARGUMENT
+
+
+def test_error_paths():
+    A = torch.zeros((1, 2048 + 4), dtype=torch.float32, device="cuda")
+    W = torch.zeros((1024, 2048), dtype=torch.int8, device="cuda")
+    S = torch.ones((1024, 32), dtype=torch.float32, device="cuda")
+    C = torch.zeros((1, 1024), dtype=torch.float32, device="cuda")
+    L = q.lib()
+    # misaligned activations (offset by one float)
+    rc = L.q3vl_linear_i8(ctypes.c_void_p(A.data_ptr() + 4), ctypes.c_void_p(W.data_ptr()),
+                          ctypes.c_void_p(S.data_ptr()), ctypes.c_void_p(C.data_ptr()),
+                          1, 1024, 2048, 64, None, 0, None)
+    assert rc == q.ERR_INVALID_ARGUMENT and "aligned" in q.last_error()
+    # K not a multiple of the group size
+    rc = L.q3vl_linear_i8(ctypes.c_void_p(A.data_ptr()), ctypes.c_void_p(W.data_ptr()),
+                          ctypes.c_void_p(S.data_ptr()), ctypes.c_void_p(C.data_ptr()),
+                          1, 1024, 2000, 64, None, 0, None)
+    assert rc == q.ERR_INVALID_ARGUMENT
+    # group size the GEMM path does not serve
+    rc = L.q3vl_linear_i8(ctypes.c_void_p(A.data_ptr()), ctypes.c_void_p(W.data_ptr()),
+                          ctypes.c_void_p(S.data_ptr()), ctypes.c_void_p(C.data_ptr()),
+                          16, 8, 1024, 16, None, 0, None)
+    assert rc == q.ERR_UNSUPPORTED
+
+
+def test_dropin_linear_host_pointers(orc):
+    """The engine's C++ linear() (host pointers, synchronous) over the GPU."""
+    lib = ctypes.CDLL(q.LINEAR_LIB_PATH)
+    import subprocess
+    sym = [l.split()[-1] for l in subprocess.run(["nm", "-D", q.LINEAR_LIB_PATH], capture_output=True,
+                                                  text=True).stdout.splitlines()
+           if l.split()[-1].startswith("_Z6linear")][0]
+    fn = getattr(lib, sym)
+    vp, sz = ctypes.c_void_p, ctypes.c_size_t
+    fn.argtypes = [vp, vp, vp, vp, vp, vp, sz, sz, sz, ctypes.c_bool, ctypes.c_int, ctypes.c_int,
+                   ctypes.c_int, ctypes.c_int, ctypes.c_bool, sz]
+    for (M, N, K) in [(1, 2048, 2048), (3, 512, 1024), (20, 256, 1024)]:
+        A, W, S = make_case(N, M, N, K, 64)
+        C = np.zeros((M, N), np.float32)
+        for _ in range(2):  # second call reuses the registered weight
+            fn(A.ctypes.data, W.ctypes.data, S.ctypes.data, None, None, C.ctypes.data, M, N, K, True,
+               q.FP32, q.INT8, q.FP32, q.FP32, True, 64)
+            assert_bits_equal(C, orc.linear(A, W, S, 64), "drop-in linear")
+    q.lib().q3vl_weight_release_all()
