@@ -41,8 +41,10 @@
  * and `workspace_bytes` (>= q3vl_workspace_bytes()). Passing NULL makes the
  * library use its own per-device buffer, grown on demand with hipMalloc
  * (not allowed while the stream is being captured into a HIP graph; capture
- * callers pass their own workspace). Calls sharing one workspace must be
- * ordered on one stream.
+ * callers pass their own workspace). A caller's workspace must be 256-byte
+ * aligned and zero-filled before its first use: its first 256 bytes hold
+ * completion counters that every call leaves at zero again. Calls sharing one
+ * workspace must be ordered on one stream.
  */
 #ifndef Q3VL_INT8_H
 #define Q3VL_INT8_H
@@ -145,6 +147,38 @@ int q3vl_argmax_rows(const float *logits, int32_t *ids, size_t M, size_t V,
 
 /* swiglu (layers/src/text_layer.cpp:420-434): gate = silu(gate) * up. */
 int q3vl_swiglu(float *gate, const float *up, size_t n, q3vl_stream stream);
+
+/* ---- the decode step that calls the int8 path (model/src/forward.cpp:
+ * 458-720): one text token through every layer and the tied lm_head, on an
+ * int8 group-quantized model held in device memory. Per-layer tensors are
+ * stacked [layers, ...] and contiguous. The KV caches are fp16
+ * [layers, kv_heads, max_seq, head_dim]. `token` and `pos` live in device
+ * memory: the call reads the token at position *pos, writes the greedy next
+ * token into *token and increments *pos, so a captured HIP graph of one call
+ * can be replayed step after step. head_dim must be 128; every linear must
+ * take the M=1 lane-ordered GEMV (dimensions >= 1024, <= 8192). */
+typedef struct q3vl_text_model {
+    int vocab, hidden, intermediate, layers, heads, kv_heads, head_dim, max_seq, group_size;
+    float rms_eps;
+    const int8_t *embed_w;      const float *embed_s;      /* [vocab, hidden], tied lm_head */
+    const int8_t *final_norm_w; const float *final_norm_s; /* [hidden] */
+    const int8_t *attn_norm_w;  const float *attn_norm_s;  /* [layers, hidden] pre-attention */
+    const int8_t *mlp_norm_w;   const float *mlp_norm_s;   /* [layers, hidden] pre-MLP */
+    const int8_t *q_norm_w;     const float *q_norm_s;     /* [layers, head_dim] */
+    const int8_t *k_norm_w;     const float *k_norm_s;     /* [layers, head_dim] */
+    const int8_t *wq, *wk, *wv, *wo, *wg, *wu, *wd;        /* [layers, N, K] */
+    const float *sq, *sk, *sv, *so, *sg, *su, *sd;         /* [layers, N, K/gs] */
+    const float *rope_cos, *rope_sin;                      /* [max_seq, head_dim/2] */
+} q3vl_text_model;
+
+/* Scratch bytes q3vl_decode_step needs for a model. */
+size_t q3vl_decode_workspace_bytes(const q3vl_text_model *m);
+
+/* One decode step; logits [vocab] are stored when non-NULL. No allocation
+ * when `workspace` is given (zero-filled before first use, as above). */
+int q3vl_decode_step(const q3vl_text_model *m, uint16_t *k_cache, uint16_t *v_cache,
+                     int32_t *token, int32_t *pos, float *logits, void *workspace,
+                     size_t workspace_bytes, q3vl_stream stream);
 
 /* ---- weight registry for host-pointer callers (the drop-in linear()).
  * The reference hands linear() mmapped host pointers to weights and scales

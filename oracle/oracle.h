@@ -56,6 +56,39 @@ void orc_swiglu(float *gate, const float *up, size_t n);
 int32_t orc_argmax(const float *logits, size_t V);
 void orc_argmax_rows(const float *logits, size_t M, size_t V, int32_t *ids);
 
+/* ---- decode step (decode_oracle.c): the int8 path's caller, forward_text */
+typedef struct orc_model {
+    int vocab, hidden, inter, layers, heads, kv_heads, head_dim, max_seq, gs;
+    float eps;
+    const int8_t *emb_w;   const float *emb_s;    /* [vocab, hidden], tied lm_head */
+    const int8_t *fnorm_w; const float *fnorm_s;  /* [hidden] final norm */
+    const int8_t *anorm_w; const float *anorm_s;  /* [L, hidden] pre-attention norm */
+    const int8_t *mnorm_w; const float *mnorm_s;  /* [L, hidden] pre-MLP norm */
+    const int8_t *qnorm_w; const float *qnorm_s;  /* [L, head_dim] */
+    const int8_t *knorm_w; const float *knorm_s;  /* [L, head_dim] */
+    const int8_t *wq, *wk, *wv, *wo, *wg, *wu, *wd;  /* [L, N, K] each */
+    const float *sq, *sk, *sv, *so, *sg, *su, *sd;   /* [L, N, K/gs] */
+    const float *rope_cos, *rope_sin;                /* [max_seq, head_dim/2] */
+} orc_model;
+
+float orc_half_to_float(uint16_t h);
+uint16_t orc_float_to_half(float f);
+float orc_sumsq(const float *x, size_t n);
+void orc_embed(const int8_t *emb_w, const float *emb_s, size_t hidden, size_t gs,
+               int32_t token, float *out);
+void orc_rms_norm_i8(const float *x, const int8_t *w, const float *ws, size_t n, size_t gs,
+                     float eps, float *out);
+void orc_rms_norm_inplace_i8(float *x, const int8_t *w, const float *ws, size_t n, size_t gs,
+                             float eps, size_t batches);
+void orc_rope(float *x, const float *cos_row, const float *sin_row, size_t heads, size_t hd);
+float orc_exp256(float x);
+void orc_softmax(float *x, size_t n);
+void orc_attention(const float *q, const float *kc, const float *vc, size_t heads,
+                   size_t kv_heads, size_t hd, size_t max_seq, size_t pos, float *att,
+                   float *out);
+int32_t orc_decode_step(const orc_model *m, void *k_cache, void *v_cache, int kv_fp16,
+                        int32_t token, size_t pos, float *logits);
+
 #ifdef __cplusplus
 }
 #endif

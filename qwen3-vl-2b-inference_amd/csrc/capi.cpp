@@ -6,6 +6,7 @@
 // (matmul/src/cpu_f32a_i8f32sb_f32c_avx2.cpp:464-475) selects its numerics.
 #include <hip/hip_runtime.h>
 
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -54,6 +55,7 @@ bool gs_ok_gemm(size_t gs) { return gs == 32 || gs == 64 || gs == 128; }
 
 // ---- workspace layout
 struct WsLayout {
+    size_t counters = 0;                  // 256 bytes, zero between calls
     size_t parts_val = 0, parts_idx = 0;  // argmax partials
     size_t aq = 0, as = 0;                // GEMM: fp16 activations, transposed scales
     size_t logits = 0;                    // lm_head M > 8 without caller logits
@@ -65,6 +67,8 @@ WsLayout layout(size_t M, size_t N, size_t K, size_t gs) {
     WsLayout L;
     size_t off = 0;
     const size_t mm = M ? M : 1;
+    L.counters = off;
+    off += 256;
     L.parts_val = off;
     off += align256(kMaxGemvParts * mm * sizeof(float));
     L.parts_idx = off;
@@ -120,6 +124,9 @@ int resolve_ws(void *user, size_t user_bytes, size_t need, char **out) {
         void *p = nullptr;
         if (hipMalloc(&p, sz) != hipSuccess)
             return fail(Q3VL_ERR_OUT_OF_MEMORY, "workspace hipMalloc(%zu) failed", sz);
+        // The counter bytes at the head of the workspace must start at zero;
+        // every call leaves them zero again.
+        Q3VL_HIP(hipMemset(p, 0, 256), "hipMemset(workspace counters)");
         g_ws.buf[dev] = p;
         g_ws.size[dev] = sz;
     }
@@ -149,8 +156,7 @@ bool gemv_path_ok(size_t M, size_t K, size_t gs) {
 // quantization followed by one GEMM per segment (M > 8).
 int run_linear(const float *A, int nseg, const int8_t *const *W, const float *const *S,
                float *const *C, int32_t *const *G, const size_t *Ns, size_t M, size_t K,
-               size_t gs, int mode, void *ws, size_t wsb, hipStream_t st, float **argmax_pv,
-               int32_t **argmax_pi, int *argmax_np) {
+               size_t gs, int mode, void *ws, size_t wsb, hipStream_t st, int32_t *ids) {
     size_t Nmax = 0;
     for (int i = 0; i < nseg; ++i) {
         int rc = check_common(A, W[i], S[i], M, Ns[i], K, gs);
@@ -158,9 +164,10 @@ int run_linear(const float *A, int nseg, const int8_t *const *W, const float *co
         if (Ns[i] > Nmax) Nmax = Ns[i];
     }
     if (M == 0 || Nmax == 0) return Q3VL_OK;
-    if (K == 0) {
+    if (K == 0) {  // the reference's general path leaves C = 0 (and argmax 0)
         for (int i = 0; i < nseg; ++i)
             if (C[i]) Q3VL_HIP(hipMemsetAsync(C[i], 0, M * Ns[i] * 4, st), "hipMemsetAsync(C)");
+        if (ids) Q3VL_HIP(hipMemsetAsync(ids, 0, M * 4, st), "hipMemsetAsync(ids)");
         return Q3VL_OK;
     }
     const WsLayout L = layout(M, Nmax, K, gs);
@@ -176,7 +183,7 @@ int run_linear(const float *A, int nseg, const int8_t *const *W, const float *co
             if (q3vl_uses_lane_path(M, Ns[i], K) != (int)lanes) {
                 for (int j = 0; j < nseg; ++j) {
                     rc = run_linear(A, 1, &W[j], &S[j], &C[j], &G[j], &Ns[j], M, K, gs,
-                                    GEMV_PLAIN, ws, wsb, st, nullptr, nullptr, nullptr);
+                                    GEMV_PLAIN, ws, wsb, st, nullptr);
                     if (rc) return rc;
                 }
                 return Q3VL_OK;
@@ -194,11 +201,9 @@ int run_linear(const float *A, int nseg, const int8_t *const *W, const float *co
         a.part_idx = reinterpret_cast<int32_t *>(wbase + L.parts_idx);
         int grid = 0;
         Q3VL_HIP(launch_gemv(a, lanes, &grid, st), "gemv launch");
-        if (argmax_pv) {
-            *argmax_pv = a.part_val;
-            *argmax_pi = a.part_idx;
-            *argmax_np = grid;
-        }
+        if (mode == GEMV_ARGMAX)
+            Q3VL_HIP(launch_argmax_final(a.part_val, a.part_idx, grid, (int)M, ids, st),
+                     "argmax final launch");
         return Q3VL_OK;
     }
 
@@ -231,15 +236,12 @@ int run_linear(const float *A, int nseg, const int8_t *const *W, const float *co
         GemmArgs g{aq, asT, (int)K, LG.lda_s, W[i], S[i], nullptr, nullptr, Ci,
                    G ? G[i] : nullptr, (int)M, (int)Ns[i], (int)K, (int)gs, false};
         Q3VL_HIP(launch_gemm(g, st), "gemm launch");
-        if (mode == GEMV_ARGMAX && argmax_pv) {
-            // Caller finishes with argmax over the logits rows.
-            *argmax_pv = reinterpret_cast<float *>(wbase + LG.parts_val);
-            *argmax_pi = reinterpret_cast<int32_t *>(wbase + LG.parts_idx);
-            *argmax_np = -1;  // signals: logits in Ci
-            Q3VL_HIP(launch_argmax_partials(Ci, (int)M, (int)Ns[i], *argmax_pv, *argmax_pi,
-                                            kGemmArgmaxParts, st),
+        if (mode == GEMV_ARGMAX)
+            Q3VL_HIP(launch_argmax_rows(Ci, (int)M, (int)Ns[i],
+                                        reinterpret_cast<float *>(wbase + LG.parts_val),
+                                        reinterpret_cast<int32_t *>(wbase + LG.parts_idx),
+                                        kGemmArgmaxParts, ids, st),
                      "argmax launch");
-        }
     }
     return Q3VL_OK;
 }
@@ -252,6 +254,83 @@ struct RegEntry {
 };
 std::mutex g_reg_mu;
 std::unordered_map<const void *, RegEntry> g_reg;
+
+// ------------------------------------------------------------ decode step
+namespace {
+
+struct DecodeLayout {
+    size_t lin;  // linear() scratch (argmax partials)
+    size_t x, t, q, k, v, ao, h, xf, scores, cmax, psum, po;
+    size_t total;
+    int max_chunks;
+};
+
+DecodeLayout decode_layout(const q3vl_text_model *m) {
+    DecodeLayout L{};
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        const size_t o = off;
+        off += align256(bytes);
+        return o;
+    };
+    const size_t H = m->hidden, I = m->intermediate, NH = m->heads, NKV = m->kv_heads,
+                 D = m->head_dim, S = m->max_seq;
+    L.max_chunks = (int)((S + kAttnChunk - 1) / kAttnChunk);
+    L.lin = take(layout(1, m->vocab, H, m->group_size).total);
+    L.x = take(H * 4);
+    L.t = take(H * 4);
+    L.q = take(NH * D * 4);
+    L.k = take(NKV * D * 4);
+    L.v = take(NKV * D * 4);
+    L.ao = take(NH * D * 4);
+    L.h = take(I * 4);
+    L.xf = take(H * 4);
+    L.scores = take(NH * S * 4);
+    L.cmax = take(NH * (size_t)L.max_chunks * 4);
+    L.psum = take(NH * (size_t)L.max_chunks * 4);
+    L.po = take(NH * (size_t)L.max_chunks * D * 4);
+    L.total = off;
+    return L;
+}
+
+int check_model(const q3vl_text_model *m) {
+    if (!m) return fail(Q3VL_ERR_INVALID_ARGUMENT, "null model");
+    const long H = m->hidden, I = m->intermediate, D = m->head_dim, gs = m->group_size;
+    if (D != 128 || m->heads <= 0 || m->kv_heads <= 0 || m->heads % m->kv_heads ||
+        m->heads / m->kv_heads > 3)
+        return fail(Q3VL_ERR_UNSUPPORTED, "decode step needs head_dim 128 and heads/kv_heads <= 3");
+    const long dims[] = {H, I, (long)m->heads * D, (long)m->kv_heads * D};
+    for (long d : dims)
+        if (d < 1024 || d > 8192 || d % 16 || !gs || d % gs)
+            return fail(Q3VL_ERR_UNSUPPORTED,
+                        "decode step needs every linear dimension in [1024, 8192], "
+                        "a multiple of 16 and of group_size (got %ld)", d);
+    if (!gs_ok_gemv((size_t)gs) || D % gs || (H & (H - 1)))
+        return fail(Q3VL_ERR_UNSUPPORTED, "group_size %ld / hidden %ld not served", gs, H);
+    if (m->vocab < 1024 || m->layers < 1 || m->max_seq < 1)
+        return fail(Q3VL_ERR_INVALID_ARGUMENT, "bad vocab / layers / max_seq");
+    const void *ptrs[] = {m->embed_w, m->embed_s, m->final_norm_w, m->final_norm_s,
+                          m->attn_norm_w, m->attn_norm_s, m->mlp_norm_w, m->mlp_norm_s,
+                          m->q_norm_w, m->q_norm_s, m->k_norm_w, m->k_norm_s, m->wq, m->wk,
+                          m->wv, m->wo, m->wg, m->wu, m->wd, m->sq, m->sk, m->sv, m->so, m->sg,
+                          m->su, m->sd, m->rope_cos, m->rope_sin};
+    for (const void *p : ptrs)
+        if (!p) return fail(Q3VL_ERR_INVALID_ARGUMENT, "null model tensor");
+    const void *w16[] = {m->embed_w, m->wq, m->wk, m->wv, m->wo, m->wg, m->wu, m->wd};
+    for (const void *p : w16)
+        if (!aligned16(p)) return fail(Q3VL_ERR_INVALID_ARGUMENT, "weights must be 16-byte aligned");
+    return Q3VL_OK;
+}
+
+GemvArgs gemv1(const float *A, int K, int gs) {
+    GemvArgs a{};
+    a.A = A;
+    a.M = 1;
+    a.K = K;
+    a.gs = gs;
+    a.mode = GEMV_PLAIN;
+    return a;
+}
 
 }  // namespace
 
@@ -308,7 +387,7 @@ int q3vl_linear_i8(const float *A, const int8_t *W, const float *S, float *C, si
     if (!C && M && N) return fail(Q3VL_ERR_INVALID_ARGUMENT, "null C");
     int32_t *G = nullptr;
     return run_linear(A, 1, &W, &S, &C, &G, &N, M, K, group_size, GEMV_PLAIN, workspace,
-                      workspace_bytes, (hipStream_t)stream, nullptr, nullptr, nullptr);
+                      workspace_bytes, (hipStream_t)stream, nullptr);
 }
 
 int q3vl_linear_i8_groups(const float *A, const int8_t *W, const float *S, float *C,
@@ -316,7 +395,7 @@ int q3vl_linear_i8_groups(const float *A, const int8_t *W, const float *S, float
                           void *workspace, size_t workspace_bytes, q3vl_stream stream) {
     if ((!C || !G) && M && N) return fail(Q3VL_ERR_INVALID_ARGUMENT, "null C or G");
     return run_linear(A, 1, &W, &S, &C, &G, &N, M, K, group_size, GEMV_PLAIN, workspace,
-                      workspace_bytes, (hipStream_t)stream, nullptr, nullptr, nullptr);
+                      workspace_bytes, (hipStream_t)stream, nullptr);
 }
 
 int q3vl_linear_i8_multi(const float *A, size_t M, size_t K, size_t group_size, int count,
@@ -329,7 +408,7 @@ int q3vl_linear_i8_multi(const float *A, size_t M, size_t K, size_t group_size, 
         if (!C[i] && M && N[i]) return fail(Q3VL_ERR_INVALID_ARGUMENT, "null C[%d]", i);
     int32_t *G[3] = {nullptr, nullptr, nullptr};
     return run_linear(A, count, W, S, C, G, N, M, K, group_size, GEMV_PLAIN, workspace,
-                      workspace_bytes, (hipStream_t)stream, nullptr, nullptr, nullptr);
+                      workspace_bytes, (hipStream_t)stream, nullptr);
 }
 
 int q3vl_linear_i8_swiglu(const float *A, const int8_t *Wg, const float *Sg, const int8_t *Wu,
@@ -343,7 +422,7 @@ int q3vl_linear_i8_swiglu(const float *A, const int8_t *Wg, const float *Sg, con
     int32_t *G[2] = {nullptr, nullptr};
     const size_t Ns[2] = {N, N};
     return run_linear(A, 2, W, S, C, G, Ns, M, K, group_size, GEMV_SWIGLU, workspace,
-                      workspace_bytes, (hipStream_t)stream, nullptr, nullptr, nullptr);
+                      workspace_bytes, (hipStream_t)stream, nullptr);
 }
 
 int q3vl_lm_head_argmax(const float *A, const int8_t *W, const float *S, float *logits,
@@ -353,18 +432,9 @@ int q3vl_lm_head_argmax(const float *A, const int8_t *W, const float *S, float *
     if (M == 0) return Q3VL_OK;
     if (V == 0 || V > 0x7fffffff)
         return fail(Q3VL_ERR_INVALID_ARGUMENT, "vocabulary size V=%zu", V);
-    hipStream_t st = (hipStream_t)stream;
-    float *pv = nullptr;
-    int32_t *pi = nullptr;
-    int np = 0;
     int32_t *G = nullptr;
-    int rc = run_linear(A, 1, &W, &S, &logits, &G, &V, M, K, group_size, GEMV_ARGMAX, workspace,
-                        workspace_bytes, st, &pv, &pi, &np);
-    if (rc) return rc;
-    if (np == -1) np = kGemmArgmaxParts;  // GEMM path: partials made from the logits
-    if (!pv || np < 1) return fail(Q3VL_ERR_INVALID_ARGUMENT, "argmax: K=0 not supported");
-    Q3VL_HIP(launch_argmax_final(pv, pi, np, (int)M, ids, st), "argmax final launch");
-    return Q3VL_OK;
+    return run_linear(A, 1, &W, &S, &logits, &G, &V, M, K, group_size, GEMV_ARGMAX, workspace,
+                      workspace_bytes, (hipStream_t)stream, ids);
 }
 
 int q3vl_argmax_rows(const float *logits, int32_t *ids, size_t M, size_t V, void *workspace,
@@ -390,6 +460,113 @@ int q3vl_swiglu(float *gate, const float *up, size_t n, q3vl_stream stream) {
     if (n == 0) return Q3VL_OK;
     if (!gate || !up) return fail(Q3VL_ERR_INVALID_ARGUMENT, "null pointer");
     Q3VL_HIP(launch_swiglu(gate, up, n, (hipStream_t)stream), "swiglu launch");
+    return Q3VL_OK;
+}
+
+size_t q3vl_decode_workspace_bytes(const q3vl_text_model *m) {
+    if (!m || m->head_dim <= 0 || m->group_size <= 0) return 0;
+    return decode_layout(m).total;
+}
+
+int q3vl_decode_step(const q3vl_text_model *m, uint16_t *k_cache, uint16_t *v_cache,
+                     int32_t *token, int32_t *pos, float *logits, void *workspace,
+                     size_t workspace_bytes, q3vl_stream stream) {
+    int rc = check_model(m);
+    if (rc) return rc;
+    if (!k_cache || !v_cache || !token || !pos)
+        return fail(Q3VL_ERR_INVALID_ARGUMENT, "null cache / token / pos");
+    const DecodeLayout L = decode_layout(m);
+    char *w = nullptr;
+    rc = resolve_ws(workspace, workspace_bytes, L.total, &w);
+    if (rc) return rc;
+    hipStream_t st = (hipStream_t)stream;
+    const int H = m->hidden, I = m->intermediate, NH = m->heads, NKV = m->kv_heads;
+    const int D = m->head_dim, gs = m->group_size, V = m->vocab;
+    const int QD = NH * D, KD = NKV * D;
+    auto F = [&](size_t off) { return reinterpret_cast<float *>(w + off); };
+    float *x = F(L.x), *t = F(L.t), *q = F(L.q), *k = F(L.k), *v = F(L.v), *ao = F(L.ao);
+    float *hb = F(L.h), *xf = F(L.xf);
+    const WsLayout LL = layout(1, V, H, gs);
+    float *pv = reinterpret_cast<float *>(w + L.lin + LL.parts_val);
+    int32_t *pi = reinterpret_cast<int32_t *>(w + L.lin + LL.parts_idx);
+
+    Q3VL_HIP(launch_embed(m->embed_w, m->embed_s, token, x, H, gs, st), "embed");  // :478-485
+    AttnArgs aa{};
+    aa.q = q;
+    aa.k = k;
+    aa.v = v;
+    aa.rope_cos = m->rope_cos;
+    aa.rope_sin = m->rope_sin;
+    aa.k_cache = k_cache;
+    aa.v_cache = v_cache;
+    aa.pos = pos;
+    aa.scores = F(L.scores);
+    aa.cmax = F(L.cmax);
+    aa.psum = F(L.psum);
+    aa.po = F(L.po);
+    aa.out = ao;
+    aa.heads = NH;
+    aa.kv_heads = NKV;
+    aa.head_dim = D;
+    aa.max_seq = m->max_seq;
+    aa.max_chunks = L.max_chunks;
+    aa.gs = gs;
+    aa.eps = m->rms_eps;
+    aa.inv_sqrt_d = 1.0f / sqrtf((float)D);  // text_layer.cpp:582
+    int grid = 0;
+    for (int l = 0; l < m->layers; ++l) {
+        const size_t lH = (size_t)l * H, lD = (size_t)l * D;
+        // :493 pre-attention RMSNorm
+        Q3VL_HIP(launch_rmsnorm_i8(x, m->attn_norm_w + lH, m->attn_norm_s + lH / gs, t, H, gs,
+                                   m->rms_eps, 0, st),
+                 "rmsnorm");
+        // :506-528 q, k, v in one GEMV launch
+        GemvArgs g = gemv1(t, H, gs);
+        g.nseg = 3;
+        g.seg[0] = {m->wq + (size_t)l * QD * H, m->sq + (size_t)l * QD * H / gs, q, nullptr, QD};
+        g.seg[1] = {m->wk + (size_t)l * KD * H, m->sk + (size_t)l * KD * H / gs, k, nullptr, KD};
+        g.seg[2] = {m->wv + (size_t)l * KD * H, m->sv + (size_t)l * KD * H / gs, v, nullptr, KD};
+        Q3VL_HIP(launch_gemv(g, true, &grid, st), "qkv gemv");
+        // :531-581 QK norm, RoPE, KV store, attention
+        aa.layer = l;
+        aa.qnorm_w = m->q_norm_w + lD;
+        aa.qnorm_s = m->q_norm_s + lD / gs;
+        aa.knorm_w = m->k_norm_w + lD;
+        aa.knorm_s = m->k_norm_s + lD / gs;
+        Q3VL_HIP(launch_attention(aa, st), "attention");
+        // :592-604 output projection, residual add into x
+        g = gemv1(ao, QD, gs);
+        g.nseg = 1;
+        g.accumulate = 1;
+        g.seg[0] = {m->wo + (size_t)l * H * QD, m->so + (size_t)l * H * QD / gs, x, nullptr, H};
+        Q3VL_HIP(launch_gemv(g, true, &grid, st), "o gemv");
+        // :611-661 pre-MLP RMSNorm, gate/up + swiglu, down, residual add
+        Q3VL_HIP(launch_rmsnorm_i8(x, m->mlp_norm_w + lH, m->mlp_norm_s + lH / gs, t, H, gs,
+                                   m->rms_eps, 0, st),
+                 "rmsnorm");
+        g = gemv1(t, H, gs);
+        g.nseg = 2;
+        g.mode = GEMV_SWIGLU;
+        g.seg[0] = {m->wg + (size_t)l * I * H, m->sg + (size_t)l * I * H / gs, hb, nullptr, I};
+        g.seg[1] = {m->wu + (size_t)l * I * H, m->su + (size_t)l * I * H / gs, nullptr, nullptr, I};
+        Q3VL_HIP(launch_gemv(g, true, &grid, st), "gate/up gemv");
+        g = gemv1(hb, I, gs);
+        g.nseg = 1;
+        g.accumulate = 1;
+        g.seg[0] = {m->wd + (size_t)l * H * I, m->sd + (size_t)l * H * I / gs, x, nullptr, H};
+        Q3VL_HIP(launch_gemv(g, true, &grid, st), "down gemv");
+    }
+    // :693-705 final RMSNorm (in place), tied classifier, greedy_decode
+    Q3VL_HIP(launch_rmsnorm_i8(x, m->final_norm_w, m->final_norm_s, xf, H, gs, m->rms_eps, 1, st),
+             "final rmsnorm");
+    GemvArgs g = gemv1(xf, H, gs);
+    g.nseg = 1;
+    g.mode = GEMV_ARGMAX;
+    g.seg[0] = {m->embed_w, m->embed_s, logits, nullptr, V};
+    g.part_val = pv;
+    g.part_idx = pi;
+    Q3VL_HIP(launch_gemv(g, true, &grid, st), "lm_head gemv");
+    Q3VL_HIP(launch_argmax_final(pv, pi, grid, 1, token, st, pos), "argmax final");
     return Q3VL_OK;
 }
 

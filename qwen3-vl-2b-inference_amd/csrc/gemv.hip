@@ -43,30 +43,150 @@ __device__ __forceinline__ float silu_mul(float gv, float uv) {
     return sl * uv;
 }
 
+// Workgroup barrier that orders LDS only: global loads stay in flight across
+// it (a full __syncthreads() waits for every outstanding global access).
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Row stride (in words) of the per-row group buffers: a multiple of 4 whose
+// quarter is odd, so 16 lanes reading 16 bytes each at consecutive rows hit
+// distinct LDS banks.
+__host__ __device__ __forceinline__ int group_ld(int Kg) {
+    const int k4 = (Kg + 3) & ~3;
+    return ((k4 >> 2) & 1) ? k4 : k4 + 4;
+}
+
+// Combine rule equivalent to the sequential strict-> scan of greedy_decode:
+// the larger value wins, equal values keep the lower index, idx<0 is empty.
+__device__ __forceinline__ void am_combine(float &bv, int32_t &bi, float v, int32_t i) {
+    if (i < 0) return;
+    if (bi < 0 || v > bv || (v == bv && i < bi)) {
+        bv = v;
+        bi = i;
+    }
+}
+
+// Segment fields held in scalar registers. The kernel never indexes
+// a.seg[] with a run-time value: that would fetch the field from kernel
+// argument memory with a vector load whose wait also drains every weight
+// load in flight.
+struct SegRegs {
+    const int8_t *W0, *W1, *W2;
+    const float *S0, *S1, *S2;
+    float *Y0, *Y1, *Y2;
+    int32_t *G0, *G1, *G2;
+    int N0, N1, N2;
+    int t1, t2;  // first tile of segments 1 and 2
+};
+
+template <typename T>
+__device__ __forceinline__ T pick3(int s, T v0, T v1, T v2) {
+    return s == 0 ? v0 : (s == 1 ? v1 : v2);
+}
+
+// Rows of one tile: row r is row tn0 + r of segment tseg (plain / argmax), or
+// row tn0 + r % (R/2) of the gate (r < R/2) or up segment (swiglu).
+struct Tile {
+    int tseg, tn0, tN;
+};
+
 template <int GS, int MR, bool LANES>
 __global__ __launch_bounds__(GEMV_MAX_THREADS) void gemv_kernel(GemvArgs a, int ntiles) {
     constexpr int T = GS / 16;
     constexpr int R = GEMV_R;
+    constexpr int HALF = R / 2;
+    // scale values per thread per tile: R*Kg <= (128/GS) * nthr since nthr >= K/16
+    constexpr int SPT = GS >= 128 ? 1 : 128 / GS;
     extern __shared__ __align__(16) unsigned char smem[];
 
     const int K = a.K;
     const int Kg = K / GS;
     const int M = a.M;
     const int tid = threadIdx.x;
-    const int nthr = blockDim.x;
-    const int g = tid / T;
+    const int nthr = blockDim.x;     // max(K/16, 64)
+    const int nchunk = K / 16;
+    const bool act = tid < nchunk;   // owns a 16-byte K-chunk
+    const int g = act ? tid / T : 0;
     const int tg = tid % T;
+    const bool swg = a.mode == GEMV_SWIGLU;
 
-    // ---- LDS carve-up
-    const int acc_words = LANES ? R * (8 * Kg + 8) : MR * R * (Kg + 1);
-    const int stage_words = acc_words > K ? acc_words : K;
+    SegRegs sr;
+    sr.W0 = a.seg[0].W; sr.W1 = a.seg[1].W; sr.W2 = a.seg[2].W;
+    sr.S0 = a.seg[0].S; sr.S1 = a.seg[1].S; sr.S2 = a.seg[2].S;
+    sr.Y0 = a.seg[0].Y; sr.Y1 = a.seg[1].Y; sr.Y2 = a.seg[2].Y;
+    sr.G0 = a.seg[0].G; sr.G1 = a.seg[1].G; sr.G2 = a.seg[2].G;
+    sr.N0 = a.seg[0].N; sr.N1 = a.seg[1].N; sr.N2 = a.seg[2].N;
+    sr.t1 = (sr.N0 + R - 1) / R;
+    sr.t2 = a.nseg > 2 ? sr.t1 + (sr.N1 + R - 1) / R : 0x7fffffff;
+    if (a.nseg < 2) sr.t1 = 0x7fffffff;
+
+    auto resolve = [&](int tile) {
+        Tile t;
+        if (swg) {
+            t.tseg = 0;
+            t.tn0 = tile * HALF;
+            t.tN = sr.N0;
+        } else {
+            t.tseg = tile < sr.t1 ? 0 : (tile < sr.t2 ? 1 : 2);
+            t.tn0 = (tile - pick3(t.tseg, 0, sr.t1, sr.t2)) * R;
+            t.tN = pick3(t.tseg, sr.N0, sr.N1, sr.N2);
+        }
+        return t;
+    };
+    auto row_seg = [&](const Tile &t, int r) { return swg ? (r < HALF ? 0 : 1) : t.tseg; };
+    auto row_n = [&](const Tile &t, int r) { return swg ? t.tn0 + (r & (HALF - 1)) : t.tn0 + r; };
+    auto row_ok = [&](const Tile &t, int r) { return row_n(t, r) < t.tN; };
+    auto seg_W = [&](int s) { return pick3(s, sr.W0, sr.W1, sr.W2); };
+    auto seg_S = [&](int s) { return pick3(s, sr.S0, sr.S1, sr.S2); };
+    auto seg_Y = [&](int s) { return pick3(s, sr.Y0, sr.Y1, sr.Y2); };
+    auto seg_G = [&](int s) { return pick3(s, sr.G0, sr.G1, sr.G2); };
+
+    // ---- LDS carve-up. accb holds the exact integer sums, one padded row of
+    // ld words per chain: [r*8 + lane][g] (lanes) or [m*R + r][g] (general).
+    const int ld = group_ld(Kg);
+    const int acc_words = (LANES ? 8 * R : MR * R) * ld;
+    // >= K (activation staging, 4 float4 per thread: 16*nthr words) and
+    // >= 2*nthr (argmax scratch)
+    int stage_words = acc_words > 16 * nthr ? acc_words : 16 * nthr;
     int32_t *accb = reinterpret_cast<int32_t *>(smem);
     float *xs = reinterpret_cast<float *>(smem);  // phase 0 only (aliases accb)
     float *as_l = reinterpret_cast<float *>(smem) + stage_words;  // [M][Kg]
-    float *sc_l = as_l + MR * Kg;                                   // [R][Kg]
-    float *ybuf = sc_l + R * Kg;                                    // [MR][R]
+    float *sc_l = as_l + MR * Kg;                                   // [R][ld]
+    float *ybuf = sc_l + R * ld;                                    // [MR][R]
 
-    // ---- phase 0: quantize the activation rows (reference i8:135-177)
+    // Weight chunk and scale prefetch for one tile (registers).
+    u32x4 wv[R];
+    float sv[SPT];
+    // Rows past the segment end and idle threads read a safe address (row 0,
+    // chunk 0) whose value is never used: no select on loaded data, so no
+    // wait is forced at issue time.
+    // Scales first, then weights: the scale fill at the top of the next
+    // iteration then waits only for the scales (vmcnt retires in order).
+    auto prefetch = [&](const Tile &t) {
+#pragma unroll
+        for (int j = 0; j < SPT; ++j) {
+            const int i = tid + j * nthr;
+            const int r = i / Kg, gg = i - (i / Kg) * Kg;
+            const bool ok = i < R * Kg && row_ok(t, r);
+            const int sg = swg ? (r < HALF ? 0 : 1) : t.tseg;
+            sv[j] = seg_S(sg)[ok ? (size_t)row_n(t, r) * Kg + gg : 0];
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const bool ok = act && row_ok(t, r);
+            const int8_t *w = seg_W(row_seg(t, r)) + (size_t)(ok ? row_n(t, r) : 0) * K + 16 * (ok ? tid : 0);
+            wv[r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(w));
+        }
+    };
+
+    int tile = blockIdx.x;
+
+    // ---- phase 0: quantize the activation rows (reference i8:135-177).
+    // Row 0's loads are issued before the first tile's weight loads so that
+    // waiting for them does not wait for the weights.
     uint32_t qp[MR][8];
 #pragma unroll
     for (int m = 0; m < MR; ++m) {
@@ -74,102 +194,80 @@ __global__ __launch_bounds__(GEMV_MAX_THREADS) void gemv_kernel(GemvArgs a, int 
         for (int j = 0; j < 8; ++j) qp[m][j] = 0;
         if (m >= M) continue;  // uniform: every thread skips together
         const float4 *src = reinterpret_cast<const float4 *>(a.A + (size_t)m * K);
-        for (int i = tid; i < K / 4; i += nthr) reinterpret_cast<float4 *>(xs)[i] = src[i];
-        __syncthreads();
-        // Every thread of a group recomputes the group's sum of squares from
-        // LDS in the reference order: 16 FMA chains over the gs/16 steps,
-        // then the fixed tree.
-        float P[16];
+        // four float4 per thread cover K/4 <= 4 * nthr (named registers; an
+        // array here ends up in scratch memory)
+        const int i0 = tid, i1 = tid + nthr, i2 = tid + 2 * nthr, i3 = tid + 3 * nthr;
+        const float4 x0 = src[i0 < K / 4 ? i0 : 0];
+        const float4 x1 = src[i1 < K / 4 ? i1 : 0];
+        const float4 x2 = src[i2 < K / 4 ? i2 : 0];
+        const float4 x3 = src[i3 < K / 4 ? i3 : 0];
+        if (m == 0) prefetch(resolve(tile));  // grid <= ntiles: every block has a tile
+        // keep the loads above ahead of the LDS stores below (the stores wait
+        // only for the activation loads, issued first); slots past K/4 exist
+        // (stage_words >= 16 * nthr) and are never read
+        __builtin_amdgcn_sched_barrier(0);
+        float4 *xs4 = reinterpret_cast<float4 *>(xs);
+        xs4[i0] = x0;
+        xs4[i1] = x1;
+        xs4[i2] = x2;
+        xs4[i3] = x3;
+        lds_barrier();
+        if (act) {
+            // Every thread of a group recomputes the group's sum of squares
+            // from LDS in the reference order: 16 FMA chains over the gs/16
+            // steps, then the fixed tree.
+            float P[16];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) P[i] = 0.0f;
-        const float *xg = xs + g * GS;
+            for (int i = 0; i < 16; ++i) P[i] = 0.0f;
+            const float *xg = xs + g * GS;
 #pragma unroll
-        for (int t = 0; t < T; ++t) {
+            for (int t = 0; t < T; ++t) {
 #pragma unroll
-            for (int i4 = 0; i4 < 4; ++i4) {
-                const float4 v = reinterpret_cast<const float4 *>(xg + 16 * t)[i4];
-                P[4 * i4 + 0] = fmaf(v.x, v.x, P[4 * i4 + 0]);
-                P[4 * i4 + 1] = fmaf(v.y, v.y, P[4 * i4 + 1]);
-                P[4 * i4 + 2] = fmaf(v.z, v.z, P[4 * i4 + 2]);
-                P[4 * i4 + 3] = fmaf(v.w, v.w, P[4 * i4 + 3]);
+                for (int i4 = 0; i4 < 4; ++i4) {
+                    const float4 v = reinterpret_cast<const float4 *>(xg + 16 * t)[i4];
+                    P[4 * i4 + 0] = fmaf(v.x, v.x, P[4 * i4 + 0]);
+                    P[4 * i4 + 1] = fmaf(v.y, v.y, P[4 * i4 + 1]);
+                    P[4 * i4 + 2] = fmaf(v.z, v.z, P[4 * i4 + 2]);
+                    P[4 * i4 + 3] = fmaf(v.w, v.w, P[4 * i4 + 3]);
+                }
+            }
+            float V[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) V[i] = P[i] + P[i + 8];
+            const float sumsq = tree8(V[0], V[1], V[2], V[3], V[4], V[5], V[6], V[7]);
+            const float s = group_scale(sumsq, 1.0f / (float)GS);
+            const float inv = rcp_rn(s);
+            if (tg == 0) as_l[m * Kg + g] = s;
+            const float *xc = xs + 16 * tid;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int32_t lo = quant_cvt(xc[2 * j] * inv);
+                const int32_t hi = quant_cvt(xc[2 * j + 1] * inv);
+                qp[m][j] = ((uint32_t)lo & 0xFFFFu) | ((uint32_t)hi << 16);
             }
         }
-        float V[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) V[i] = P[i] + P[i + 8];
-        const float sumsq = tree8(V[0], V[1], V[2], V[3], V[4], V[5], V[6], V[7]);
-        const float s = group_scale(sumsq, 1.0f / (float)GS);
-        const float inv = rcp_rn(s);
-        if (tg == 0) as_l[m * Kg + g] = s;
-        const float *xc = xs + 16 * tid;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int32_t lo = quant_cvt(xc[2 * j] * inv);
-            const int32_t hi = quant_cvt(xc[2 * j + 1] * inv);
-            qp[m][j] = ((uint32_t)lo & 0xFFFFu) | ((uint32_t)hi << 16);
-        }
-        __syncthreads();
+        lds_barrier();
     }
 
-    // Running argmax of activation row `tid` (threads tid < M), over the
-    // block's tiles in ascending row order.
+    // Running argmax (argmax mode) of the block's tiles, in ascending row
+    // order, held by the lane that leads each activation row's chain group.
     float best = -FLT_MAX;
     int32_t bidx = -1;
 
-    const int half = R / 2;
-    for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
-        // ---- resolve the tile's rows: row r of the tile is row tn0 + r of
-        // segment tseg (plain / argmax), or row tn0 + r % (R/2) of the gate
-        // (r < R/2) or up segment (swiglu).
-        const bool swg = a.mode == GEMV_SWIGLU;
-        int tseg = 0, tn0;
-        if (swg) {
-            tn0 = tile * half;
-        } else {
-            int t0 = tile;
-            while (tseg + 1 < a.nseg) {
-                const int ts = (a.seg[tseg].N + R - 1) / R;
-                if (t0 < ts) break;
-                t0 -= ts;
-                ++tseg;
-            }
-            tn0 = t0 * R;
-        }
-        const int tN = a.seg[tseg].N;
-        auto row_seg = [&](int r) { return swg ? (r < half ? 0 : 1) : tseg; };
-        auto row_n = [&](int r) { return swg ? tn0 + (r & (half - 1)) : tn0 + r; };
-        auto row_ok = [&](int r) { return row_n(r) < tN; };
-        bool valid[R];
-        const int8_t *wrow[R];
+    Tile cur = resolve(tile);
+    for (; tile < ntiles; tile += gridDim.x) {
+        // ---- scales of the tile's rows -> LDS (values already in sv)
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-            valid[r] = row_ok(r);
-            wrow[r] = a.seg[row_seg(r)].W + (size_t)(valid[r] ? row_n(r) : 0) * K;
-        }
-
-        // ---- issue all weight loads of the tile
-        u32x4 wv[R];
-#pragma unroll
-        for (int r = 0; r < R; ++r)
-            wv[r] = valid[r] ? __builtin_nontemporal_load(
-                                   reinterpret_cast<const u32x4 *>(wrow[r]) + tid)
-                             : (u32x4){0u, 0u, 0u, 0u};
-
-        // ---- scales of the tile's rows -> LDS
-        for (int i = tid; i < R * Kg; i += nthr) {
-            const int r = i / Kg, gg = i - r * Kg;
-            float v = 0.0f;
-            if (row_ok(r)) {
-                const float ws = a.seg[row_seg(r)].S[(size_t)row_n(r) * Kg + gg];
-                v = LANES ? as_l[gg] * ws : ws;  // i8:213 a_s * w_s (lanes)
-            }
-            sc_l[i] = v;
+        for (int j = 0; j < SPT; ++j) {
+            const int i = tid + j * nthr;
+            const int r = i / Kg, gg = i - (i / Kg) * Kg;
+            if (i < R * Kg) sc_l[r * ld + gg] = LANES ? as_l[gg] * sv[j] : sv[j];  // i8:213
         }
 
         // ---- phase 1: exact integer lane / group sums
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            if (!valid[r]) continue;  // uniform across the block
+            if (!row_ok(cur, r)) continue;  // uniform across the block
             const uint32_t wd[4] = {wv[r].x, wv[r].y, wv[r].z, wv[r].w};
             uint32_t wp[8];
 #pragma unroll
@@ -177,20 +275,19 @@ __global__ __launch_bounds__(GEMV_MAX_THREADS) void gemv_kernel(GemvArgs a, int 
                 wp[2 * d] = lo2(wd[d]);
                 wp[2 * d + 1] = hi2(wd[d]);
             }
+            int32_t *Gd = seg_G(row_seg(cur, r));
             if constexpr (LANES) {
                 int32_t p[8];
 #pragma unroll
                 for (int j = 0; j < 8; ++j) p[j] = run_sum<T>(dot2(qp[0][j], wp[j], 0));
-                if (tg == 0) {
-                    int4 *dst = reinterpret_cast<int4 *>(accb + r * (8 * Kg + 8) + 8 * g);
-                    dst[0] = make_int4(p[0] >> 8, p[1] >> 8, p[2] >> 8, p[3] >> 8);
-                    dst[1] = make_int4(p[4] >> 8, p[5] >> 8, p[6] >> 8, p[7] >> 8);
-                    int32_t *Gd = a.seg[row_seg(r)].G;
+                if (act && tg == 0) {
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) accb[(r * 8 + j) * ld + g] = p[j] >> 8;
                     if (Gd) {
                         int32_t tot = 0;
 #pragma unroll
                         for (int j = 0; j < 8; ++j) tot += p[j] >> 8;
-                        Gd[(size_t)row_n(r) * Kg + g] = tot;
+                        Gd[(size_t)row_n(cur, r) * Kg + g] = tot;
                     }
                 }
             } else {
@@ -201,15 +298,22 @@ __global__ __launch_bounds__(GEMV_MAX_THREADS) void gemv_kernel(GemvArgs a, int 
 #pragma unroll
                     for (int j = 0; j < 8; ++j) acc = dot2(qp[m][j], wp[j], acc);
                     acc = run_sum<T>(acc >> 8);
-                    if (tg == 0) {
-                        accb[(m * R + r) * (Kg + 1) + g] = acc;
-                        int32_t *Gd = a.seg[row_seg(r)].G;
-                        if (Gd) Gd[((size_t)m * tN + row_n(r)) * Kg + g] = acc;
+                    if (act && tg == 0) {
+                        accb[(m * R + r) * ld + g] = acc;
+                        if (Gd) Gd[((size_t)m * cur.tN + row_n(cur, r)) * Kg + g] = acc;
                     }
                 }
             }
         }
-        __syncthreads();
+
+        // ---- prefetch the next tile while this one finishes
+        const Tile t = cur;
+        const int nxt = tile + gridDim.x;
+        if (nxt < ntiles) {
+            cur = resolve(nxt);
+            prefetch(cur);
+        }
+        lds_barrier();
 
         // ---- phase 2: fp32 group chains in the reference order
         float y = 0.0f;
@@ -219,87 +323,109 @@ __global__ __launch_bounds__(GEMV_MAX_THREADS) void gemv_kernel(GemvArgs a, int 
             if (tid < 8 * R) {
                 const int r = tid >> 3, j = tid & 7;
                 float c = 0.0f;
-                if (row_ok(r)) {
-                    const int32_t *Lr = accb + r * (8 * Kg + 8) + j;
-                    const float *scr = sc_l + r * Kg;
-                    for (int gg = 0; gg < Kg; ++gg)
-                        c = fmaf((float)Lr[8 * gg], scr[gg], c);  // i8:213-216
+                if (row_ok(t, r)) {
+                    const int32_t *Lr = accb + tid * ld;
+                    const float *scr = sc_l + r * ld;
+                    int gg = 0;
+#pragma unroll 2
+                    for (; gg + 4 <= Kg; gg += 4) {
+                        const int4 L4 = *reinterpret_cast<const int4 *>(Lr + gg);
+                        const float4 s4 = *reinterpret_cast<const float4 *>(scr + gg);
+                        c = fmaf((float)L4.x, s4.x, c);  // i8:213-216, groups in order
+                        c = fmaf((float)L4.y, s4.y, c);
+                        c = fmaf((float)L4.z, s4.z, c);
+                        c = fmaf((float)L4.w, s4.w, c);
+                    }
+                    for (; gg < Kg; ++gg) c = fmaf((float)Lr[gg], scr[gg], c);
                 }
                 // add_reduce_mm_256 over the row's 8 lanes (i8:219-222).
                 c = c + __shfl_xor(c, 4, 8);
                 c = c + __shfl_xor(c, 1, 8);
                 c = c + __shfl_xor(c, 2, 8);
                 y = c;
-                ym = 0;
                 yr = r;
-                yvalid = (j == 0) && row_ok(r);
+                yvalid = (j == 0) && row_ok(t, r);
             }
         } else {
             if (tid < M * R) {
                 const int m = tid / R, r = tid - (tid / R) * R;
                 float acc = 0.0f;
-                if (row_ok(r)) {
-                    const int32_t *Gr = accb + (m * R + r) * (Kg + 1);
+                if (row_ok(t, r)) {
+                    const int32_t *Gr = accb + (m * R + r) * ld;
                     const float *asr = as_l + m * Kg;
-                    const float *wsr = sc_l + r * Kg;
-                    for (int gg = 0; gg < Kg; ++gg) {
-                        const float ga = (float)Gr[gg] * asr[gg];
-                        acc = fmaf(ga, wsr[gg], acc);  // i8:613-617 (contracted)
+                    const float *wsr = sc_l + r * ld;
+                    int gg = 0;
+#pragma unroll 2
+                    for (; gg + 4 <= Kg; gg += 4) {
+                        const int4 G4 = *reinterpret_cast<const int4 *>(Gr + gg);
+                        const float4 w4 = *reinterpret_cast<const float4 *>(wsr + gg);
+                        // i8:613-617 (contracted): acc = fma(G*a_s, w_s, acc)
+                        acc = fmaf((float)G4.x * asr[gg + 0], w4.x, acc);
+                        acc = fmaf((float)G4.y * asr[gg + 1], w4.y, acc);
+                        acc = fmaf((float)G4.z * asr[gg + 2], w4.z, acc);
+                        acc = fmaf((float)G4.w * asr[gg + 3], w4.w, acc);
                     }
+                    for (; gg < Kg; ++gg) acc = fmaf((float)Gr[gg] * asr[gg], wsr[gg], acc);
                 }
                 y = acc;
                 ym = m;
                 yr = r;
-                yvalid = row_ok(r);
+                yvalid = row_ok(t, r);
             }
         }
 
         // ---- epilogues
         if (a.mode == GEMV_PLAIN) {
-            if (yvalid) a.seg[row_seg(yr)].Y[(size_t)ym * tN + row_n(yr)] = y;
-        } else {
+            // plain mode: every row of a tile is in segment t.tseg
+            if (yvalid) {
+                float *dst = seg_Y(t.tseg) + (size_t)ym * t.tN + row_n(t, yr);
+                *dst = a.accumulate ? *dst + y : y;  // add_vector: to[i] += from[i]
+            }
+        } else if (swg) {
             if (yvalid) ybuf[ym * R + yr] = y;
-            __syncthreads();
-            if (a.mode == GEMV_SWIGLU) {
-                if (tid < M * half) {
-                    const int m = tid / half, r = tid - (tid / half) * half;
-                    if (row_ok(r))
-                        a.seg[0].Y[(size_t)m * tN + row_n(r)] =
-                            silu_mul(ybuf[m * R + r], ybuf[m * R + r + half]);
-                }
-            } else {  // GEMV_ARGMAX
-                if (tid < M) {
-                    const int m = tid;
-                    for (int r = 0; r < R; ++r) {
-                        if (!row_ok(r)) break;
-                        const float v = ybuf[m * R + r];
-                        if (a.seg[0].Y) a.seg[0].Y[(size_t)m * tN + row_n(r)] = v;
-                        // greedy_decode (tokenizer/src/utils.cpp:34-44): strict >
-                        if (v > best) {
-                            best = v;
-                            bidx = row_n(r);
-                        }
-                    }
-                }
+            lds_barrier();
+            if (tid < M * HALF) {
+                const int m = tid / HALF, r = tid - (tid / HALF) * HALF;
+                if (row_ok(t, r))
+                    sr.Y0[(size_t)m * t.tN + row_n(t, r)] =
+                        silu_mul(ybuf[m * R + r], ybuf[m * R + r + HALF]);
+            }
+        } else {  // GEMV_ARGMAX, in registers of the wave that holds y
+            if (yvalid && sr.Y0) sr.Y0[(size_t)ym * t.tN + row_n(t, yr)] = y;
+            // candidate: a valid row whose value beats -FLT_MAX (NaN never)
+            float cv = y;
+            int32_t ci = (yvalid && y > -FLT_MAX) ? row_n(t, yr) : -1;
+            // The tile's rows of one activation row sit in R lanes spaced by
+            // RS (lanes: rows are 8 lanes apart; general: adjacent lanes).
+            constexpr int RS = LANES ? 8 : 1;
+#pragma unroll
+            for (int off = RS; off < RS * R; off <<= 1) {
+                const float ov = __shfl_xor(cv, off);
+                const int32_t oi = __shfl_xor(ci, off);
+                am_combine(cv, ci, ov, oi);  // larger value, then lower index
+            }
+            // Rows of later tiles have larger indices: a strict > keeps the
+            // first occurrence, as greedy_decode's scan does.
+            if (tid < M * R * RS && (tid & (RS * R - 1)) == 0 && ci >= 0 &&
+                (bidx < 0 || cv > best)) {
+                best = cv;
+                bidx = ci;
             }
         }
-        __syncthreads();
+        lds_barrier();
     }
 
-    if (a.mode == GEMV_ARGMAX && tid < M) {
-        a.part_val[(size_t)blockIdx.x * M + tid] = best;
-        a.part_idx[(size_t)blockIdx.x * M + tid] = bidx;
-    }
-}
-
-// ----------------------------------------------------------------- argmax
-// Combine rule equivalent to the sequential strict-> scan: the larger value
-// wins, equal values keep the lower index, candidates with idx<0 are empty.
-__device__ __forceinline__ void am_combine(float &bv, int32_t &bi, float v, int32_t i) {
-    if (i < 0) return;
-    if (bi < 0 || v > bv || (v == bv && i < bi)) {
-        bv = v;
-        bi = i;
+    if (a.mode != GEMV_ARGMAX) return;
+    // ---- argmax: this block's (value, index) partial per activation row, in
+    // its own slots (no shared counters or atomics: 2048 blocks contending on
+    // one address serialize); argmax_final_kernel reduces the partials.
+    // The running best of activation row m lives on lane m*R (general) or
+    // lane 0 (lanes, M == 1).
+    const int lead = LANES ? 0 : (tid % R == 0 && tid < M * R ? tid / R : -1);
+    if ((LANES ? tid == 0 : lead >= 0)) {
+        const int m = LANES ? 0 : lead;
+        a.part_val[(size_t)blockIdx.x * M + m] = best;
+        a.part_idx[(size_t)blockIdx.x * M + m] = bidx;
     }
 }
 
@@ -325,16 +451,46 @@ __device__ void am_block_reduce(float &bv, int32_t &bi) {
     __syncthreads();
 }
 
-__global__ __launch_bounds__(256) void argmax_final_kernel(const float *pv, const int32_t *pi,
-                                                           int nparts, int M, int32_t *ids) {
+// Reduces block partials [nparts, M] to ids[m] (empty partials have idx < 0;
+// none at all -> 0, as greedy_decode returns 0 when nothing beats -FLT_MAX).
+// 1024 threads, each issuing all of its (<= 8) loads before combining.
+__global__ __launch_bounds__(1024) void argmax_final_kernel(const float *pv, const int32_t *pi,
+                                                            int nparts, int M, int32_t *ids,
+                                                            int32_t *pos_inc) {
+    __shared__ float wv[16];
+    __shared__ int32_t wi[16];
+    const int tid = threadIdx.x;
     for (int m = 0; m < M; ++m) {
+        float v[8];
+        int32_t ix[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int p = tid + u * 1024;
+            v[u] = p < nparts ? pv[(size_t)p * M + m] : -FLT_MAX;
+            ix[u] = p < nparts ? pi[(size_t)p * M + m] : -1;
+        }
         float bv = -FLT_MAX;
         int32_t bi = -1;
-        for (int p = threadIdx.x; p < nparts; p += blockDim.x)
-            am_combine(bv, bi, pv[(size_t)p * M + m], pi[(size_t)p * M + m]);
-        am_block_reduce(bv, bi);
-        if (threadIdx.x == 0) ids[m] = bi < 0 ? 0 : bi;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) am_combine(bv, bi, v[u], ix[u]);
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+            const float ov = __shfl_xor(bv, off);
+            const int32_t oi = __shfl_xor(bi, off);
+            am_combine(bv, bi, ov, oi);
+        }
+        if ((tid & 63) == 0) {
+            wv[tid >> 6] = bv;
+            wi[tid >> 6] = bi;
+        }
+        __syncthreads();
+        if (tid == 0) {
+            for (int w = 1; w < 16; ++w) am_combine(bv, bi, wv[w], wi[w]);
+            ids[m] = bi < 0 ? 0 : bi;
+        }
+        __syncthreads();
     }
+    if (tid == 0 && pos_inc) *pos_inc += 1;
 }
 
 // Stand-alone argmax over logits rows: block b scans a contiguous slice with
@@ -368,10 +524,11 @@ template <int GS, int MR, bool LANES>
 static hipError_t launch_gemv_t(const GemvArgs &a, int *grid_out, hipStream_t st) {
     constexpr int R = GEMV_R;
     const int K = a.K, Kg = K / GS;
-    const int nthr = K / 16;
-    const int acc_words = LANES ? R * (8 * Kg + 8) : MR * R * (Kg + 1);
-    const int stage_words = acc_words > K ? acc_words : K;
-    const size_t lds = (size_t)(stage_words + MR * Kg + R * Kg + MR * R) * 4;
+    const int nthr = K / 16 > 64 ? K / 16 : 64;
+    const int ld = group_ld(Kg);
+    const int acc_words = (LANES ? 8 * R : MR * R) * ld;
+    const int stage_words = acc_words > 16 * nthr ? acc_words : 16 * nthr;
+    const size_t lds = (size_t)(stage_words + MR * Kg + R * ld + MR * R) * 4;
 
     int ntiles = 0;
     if (a.mode == GEMV_SWIGLU) {
@@ -419,8 +576,9 @@ hipError_t launch_gemv(const GemvArgs &a, bool lanes, int *grid_out, hipStream_t
 }
 
 hipError_t launch_argmax_final(const float *pv, const int32_t *pi, int nparts, int M,
-                               int32_t *ids, hipStream_t st) {
-    argmax_final_kernel<<<1, 256, 0, st>>>(pv, pi, nparts, M, ids);
+                               int32_t *ids, hipStream_t st, int32_t *pos_inc) {
+    if (nparts > 8192) return hipErrorInvalidValue;
+    argmax_final_kernel<<<1, 1024, 0, st>>>(pv, pi, nparts, M, ids, pos_inc);
     return hipGetLastError();
 }
 

@@ -37,6 +37,7 @@ struct GemvArgs {
     int nseg;
     int M, K, gs;
     int mode;
+    int accumulate;   // GEMV_PLAIN: Y += A W^T (the decode step's residual add)
     float *part_val;  // GEMV_ARGMAX: [grid, M] block partial maxima
     int32_t *part_idx;  // [grid, M] block partial indices (-1: none)
 };
@@ -47,9 +48,11 @@ struct GemvArgs {
 // Returns the grid size used (argmax partial count) through *grid_out.
 hipError_t launch_gemv(const GemvArgs &a, bool lanes, int *grid_out, hipStream_t st);
 
-// Final argmax over block partials: ids[m] = first index of the maximum.
+// Final argmax over block partials: ids[m] = first index of the maximum;
+// *pos_inc += 1 afterwards when pos_inc is non-null (decode step position).
 hipError_t launch_argmax_final(const float *part_val, const int32_t *part_idx,
-                               int nparts, int M, int32_t *ids, hipStream_t st);
+                               int nparts, int M, int32_t *ids, hipStream_t st,
+                               int32_t *pos_inc = nullptr);
 // Block partials of greedy argmax over rows of logits ([nparts, M] layout).
 hipError_t launch_argmax_partials(const float *logits, int M, int V, float *part_val,
                                   int32_t *part_idx, int nparts, hipStream_t st);
@@ -59,6 +62,27 @@ hipError_t launch_argmax_rows(const float *logits, int M, int V, float *part_val
                               hipStream_t st);
 // Stand-alone swiglu: gate[i] = silu(gate[i]) * up[i].
 hipError_t launch_swiglu(float *gate, const float *up, size_t n, hipStream_t st);
+
+// ------------------------------------------------------------ decode step
+struct AttnArgs {
+    const float *q, *k, *v;                 // raw projections [heads*hd], [kv_heads*hd]
+    const int8_t *qnorm_w, *knorm_w;        // this layer's [hd] int8 norm weights
+    const float *qnorm_s, *knorm_s;
+    const float *rope_cos, *rope_sin;       // [max_seq, hd/2]
+    uint16_t *k_cache, *v_cache;            // fp16 [layers, kv_heads, max_seq, hd]
+    const int32_t *pos;                     // device: position of the new token
+    float *scores, *cmax, *psum, *po;       // scratch
+    float *out;                             // [heads*hd]
+    int layer, heads, kv_heads, head_dim, max_seq, max_chunks, gs;
+    float eps, inv_sqrt_d;
+};
+hipError_t launch_embed(const int8_t *w, const float *s, const int32_t *token, float *x, int H,
+                        int gs, hipStream_t st);
+// mode 0: rms_norm (fp64 inverse root); mode 1: rms_norm_inplace (fp32)
+hipError_t launch_rmsnorm_i8(const float *x, const int8_t *w, const float *ws, float *out, int n,
+                             int gs, float eps, int mode, hipStream_t st);
+hipError_t launch_attention(const AttnArgs &a, hipStream_t st);
+constexpr int kAttnChunk = 64;  // positions per attention work chunk
 
 // ---------------------------------------------------------- GEMM (MFMA)
 struct GemmArgs {

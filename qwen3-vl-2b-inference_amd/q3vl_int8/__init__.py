@@ -141,8 +141,10 @@ def _ws(workspace):
 
 
 def alloc_workspace(M, N, K, gs, device="cuda"):
+    """Zero-filled device workspace (its head holds counters that must start
+    at zero; every call leaves them zero)."""
     torch = _torch()
-    return torch.empty(workspace_bytes(M, N, K, gs), dtype=torch.uint8, device=device)
+    return torch.zeros(workspace_bytes(M, N, K, gs), dtype=torch.uint8, device=device)
 
 
 def quantize_rows(A, gs, q=None, a_s=None, stream=None):

@@ -149,9 +149,12 @@ def test_swiglu_fused_parity(orc, M, N, K):
     g = orc.linear(A, Wg, Sg, gs)
     u = orc.linear(A, Wu, Su, gs)
     H_ref = orc.swiglu(g, u)
-    # tolerance: expf rounding may differ by 1 ulp from libm; everything else exact
+    # Tolerance: the gate/up linears are bit-exact; silu's expf is correctly
+    # rounded here while glibc's expf is not always (<= 1 ulp apart), which
+    # g/(1+e)*u can grow to a few ulp: allow 4 ulp / 1e-6 relative.
     d = ulp_diff(H, H_ref)
-    assert d.max() <= 2, d.max()
+    assert d.max() <= 4, d.max()
+    np.testing.assert_allclose(H, H_ref, rtol=1e-6, atol=0)
     assert (d == 0).mean() > 0.999
 
 
@@ -159,8 +162,8 @@ def test_swiglu_standalone(orc):
     from golden.make_golden import swiglu_inputs
     g, u = swiglu_inputs()
     out = host(q.swiglu(dev(g), dev(u)))
-    d = ulp_diff(out, orc.swiglu(g, u))
-    assert d.max() <= 2 and (d == 0).mean() > 0.999
+    d = ulp_diff(out, orc.swiglu(g, u))  # tolerance as in test_swiglu_fused_parity
+    assert d.max() <= 4 and (d == 0).mean() > 0.999
 
 
 @pytest.mark.parametrize("M", [1, 8])
