@@ -256,8 +256,6 @@ std::mutex g_reg_mu;
 std::unordered_map<const void *, RegEntry> g_reg;
 
 // ------------------------------------------------------------ decode step
-namespace {
-
 struct DecodeLayout {
     size_t lin;  // linear() scratch (argmax partials)
     size_t x, t, q, k, v, ao, h, xf, scores, cmax, psum, po;
