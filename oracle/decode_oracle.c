@@ -7,12 +7,11 @@
  * Reference files: layers/src/text_layer.cpp ("tl:"), layers/include/
  * simd_utils.hpp ("ls:"), model/src/load_model.cpp ("lm:").
  *
- * Fixed orders chosen here where the reference leaves the order to the
- * compiler (`#pragma omp simd reduction`): the sum of squares of the RMS norms
- * (tl:120-124, 248-252) and the dot product of the last (tail) attention
- * positions (tl:626-633). Both are pinned against the compiled reference to a
- * tolerance, not bit for bit; everything else follows the reference's explicit
- * operation order.
+ * Where the reference leaves the order to the compiler (`#pragma omp simd
+ * reduction`), the tail attention positions (tl:626-633) follow GCC's AVX2
+ * vectorization (identified against the compiled reference), and the RMS sum
+ * of squares (tl:120-124, 248-252) uses this build's fixed order (pinned to a
+ * tolerance). Everything else follows the reference's explicit order.
  */
 #include <float.h>
 #include <math.h>
@@ -76,20 +75,20 @@ uint16_t orc_float_to_half(float f) {
 
 /* ---------------------------------------------------------- building blocks */
 
-/* Sum of squares in this build's fixed order: 256 FMA chains (chain c takes
- * x[c], x[c+256], ...) folded by a binary tree (c += c + w for w = 128..1).
- * For n < 256 the chain count is n (n a power of two). */
+/* Sum of squares in the order the reference's `omp simd reduction(+:ss)`
+ * loops take (tl:121-124, tl:247-250, compiled for 8-wide AVX2): lane l
+ * accumulates x[j]*x[j] for j = l (mod 8) with one FMA per term, then the
+ * lanes are folded left to right, ((c0 + c1) + c2) + ... + c7. Terms past the
+ * last multiple of 8 are added after the fold, one FMA each. */
 float orc_sumsq(const float *x, size_t n) {
-    float p[256];
-    const size_t C = n < 256 ? n : 256;
-    for (size_t c = 0; c < C; ++c) {
-        float s = 0.0f;
-        for (size_t j = c; j < n; j += C) s = fmaf(x[j], x[j], s);
-        p[c] = s;
-    }
-    for (size_t w = C / 2; w >= 1; w /= 2)
-        for (size_t c = 0; c < w; ++c) p[c] = p[c] + p[c + w];
-    return p[0];
+    float c[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    const size_t n8 = n & ~(size_t)7;
+    for (size_t j = 0; j < n8; j += 8)
+        for (int l = 0; l < 8; ++l) c[l] = fmaf(x[j + l], x[j + l], c[l]);
+    float s = c[0];
+    for (int l = 1; l < 8; ++l) s = s + c[l];
+    for (size_t j = n8; j < n; ++j) s = fmaf(x[j], x[j], s);
+    return s;
 }
 
 /* tl:3-49 embedding_lookup, int8 group-quantized branch. */
@@ -100,13 +99,14 @@ void orc_embed(const int8_t *emb_w, const float *emb_s, size_t hidden, size_t gs
     for (size_t i = 0; i < hidden; ++i) out[i] = (float)w[i] * s[i / gs];
 }
 
-/* tl:110-147 rms_norm, int8 group-quantized weight, one row:
- * inv = (float)(1 / sqrt((double)(ss/n + eps))), out = w * ((s_g * inv) * x). */
+/* tl:110-147 rms_norm, int8 group-quantized weight, one row. The argument of
+ * sqrt is a float, so the float overload is taken: inv = (float)(1.0 /
+ * (double)sqrtf(ss/n + eps)), out = w * ((s_g * inv) * x). */
 void orc_rms_norm_i8(const float *x, const int8_t *w, const float *ws, size_t n, size_t gs,
                      float eps, float *out) {
     const float ss = orc_sumsq(x, n);
     const float inv_hs = 1.0f / (float)n;
-    const float inv = (float)(1.0 / sqrt((double)(ss * inv_hs + eps)));
+    const float inv = (float)(1.0 / (double)sqrtf(ss * inv_hs + eps));
     for (size_t g = 0; g < n; g += gs) {
         const float combined = ws[g / gs] * inv;
         for (size_t j = g; j < g + gs; ++j) out[j] = (float)w[j] * (combined * x[j]);
@@ -212,14 +212,26 @@ void orc_softmax(float *x, size_t n) {
 }
 
 /* 8 FMA lane chains over the head dimension then the fixed 8-lane tree
- * (tl:598-620 with add_reduce_mm_256_layer); also used for the tail
- * positions, whose order the reference leaves to the compiler. */
+ * (tl:598-620 with add_reduce_mm_256_layer). */
 static float dot_lanes(const float *q, const float *k, size_t hd) {
     float c[8] = {0};
     for (size_t i = 0; i < hd; i += 8)
         for (int l = 0; l < 8; ++l) c[l] = fmaf(q[i + l], k[i + l], c[l]);
     const float s0 = c[0] + c[4], s1 = c[1] + c[5], s2 = c[2] + c[6], s3 = c[3] + c[7];
     return (s0 + s1) + (s2 + s3);
+}
+
+/* Tail positions (tl:626-633): `#pragma omp simd reduction(+:score)` over
+ * score += q[i]*k[i], restated as GCC's AVX2 vectorization of it: the same 8
+ * FMA lane chains, then the lanes added in order l0 + l1 + ... + l7
+ * (identified against the compiled reference on all-tail probes). */
+static float dot_tail(const float *q, const float *k, size_t hd) {
+    float c[8] = {0};
+    for (size_t i = 0; i < hd; i += 8)
+        for (int l = 0; l < 8; ++l) c[l] = fmaf(q[i + l], k[i + l], c[l]);
+    float s = c[0];
+    for (int l = 1; l < 8; ++l) s = s + c[l];
+    return s;
 }
 
 /* tl:575-650 attn_scores_all_heads + softmax, and tl:655-710
@@ -235,7 +247,11 @@ void orc_attention(const float *q, const float *kc, const float *vc, size_t head
         const float *qh = q + h * hd;
         const float *kh = kc + (h / kv_mul) * max_seq * hd;
         const float *vh = vc + (h / kv_mul) * max_seq * hd;
+        /* main loop: blocks of 8 positions with t + 8 <= pos (tl:593-622);
+         * the tail loop then recomputes t in [pos/8*8, pos] (tl:626-634) */
         for (size_t t = 0; t <= pos; ++t) att[t] = dot_lanes(qh, kh + t * hd, hd) * inv_sqrt_d;
+        for (size_t t = pos / 8 * 8; t <= pos; ++t)
+            att[t] = dot_tail(qh, kh + t * hd, hd) * inv_sqrt_d;
         orc_softmax(att, pos + 1);
         float *oh = out + h * hd;
         for (size_t d = 0; d < hd; ++d) {

@@ -258,7 +258,7 @@ std::unordered_map<const void *, RegEntry> g_reg;
 // ------------------------------------------------------------ decode step
 struct DecodeLayout {
     size_t lin;  // linear() scratch (argmax partials)
-    size_t x, t, q, k, v, ao, h, xf, scores, cmax, psum, po;
+    size_t x, t, q, k, v, ao, h, xf, scores, cmax;
     size_t total;
     int max_chunks;
 };
@@ -285,8 +285,6 @@ DecodeLayout decode_layout(const q3vl_text_model *m) {
     L.xf = take(H * 4);
     L.scores = take(NH * S * 4);
     L.cmax = take(NH * (size_t)L.max_chunks * 4);
-    L.psum = take(NH * (size_t)L.max_chunks * 4);
-    L.po = take(NH * (size_t)L.max_chunks * D * 4);
     L.total = off;
     return L;
 }
@@ -303,10 +301,14 @@ int check_model(const q3vl_text_model *m) {
             return fail(Q3VL_ERR_UNSUPPORTED,
                         "decode step needs every linear dimension in [1024, 8192], "
                         "a multiple of 16 and of group_size (got %ld)", d);
-    if (!gs_ok_gemv((size_t)gs) || D % gs || (H & (H - 1)))
-        return fail(Q3VL_ERR_UNSUPPORTED, "group_size %ld / hidden %ld not served", gs, H);
-    if (m->vocab < 1024 || m->layers < 1 || m->max_seq < 1)
-        return fail(Q3VL_ERR_INVALID_ARGUMENT, "bad vocab / layers / max_seq");
+    if (!gs_ok_gemv((size_t)gs) || D % gs)
+        return fail(Q3VL_ERR_UNSUPPORTED, "group_size %ld not served", gs);
+    if (m->vocab < 1024 || m->layers < 1 || m->max_seq < 8 || m->max_seq % 8)
+        return fail(Q3VL_ERR_INVALID_ARGUMENT, "bad vocab / layers / max_seq (a multiple of 8)");
+    if (attention_lds_bytes(m->heads, m->kv_heads, m->max_seq) > kAttnMaxLds)
+        return fail(Q3VL_ERR_UNSUPPORTED,
+                    "max_seq %d too long for the attention kernel's LDS (heads/kv_heads %d)",
+                    m->max_seq, m->heads / m->kv_heads);
     const void *ptrs[] = {m->embed_w, m->embed_s, m->final_norm_w, m->final_norm_s,
                           m->attn_norm_w, m->attn_norm_s, m->mlp_norm_w, m->mlp_norm_s,
                           m->q_norm_w, m->q_norm_s, m->k_norm_w, m->k_norm_s, m->wq, m->wk,
@@ -500,8 +502,6 @@ int q3vl_decode_step(const q3vl_text_model *m, uint16_t *k_cache, uint16_t *v_ca
     aa.pos = pos;
     aa.scores = F(L.scores);
     aa.cmax = F(L.cmax);
-    aa.psum = F(L.psum);
-    aa.po = F(L.po);
     aa.out = ao;
     aa.heads = NH;
     aa.kv_heads = NKV;
@@ -516,7 +516,7 @@ int q3vl_decode_step(const q3vl_text_model *m, uint16_t *k_cache, uint16_t *v_ca
         const size_t lH = (size_t)l * H, lD = (size_t)l * D;
         // :493 pre-attention RMSNorm
         Q3VL_HIP(launch_rmsnorm_i8(x, m->attn_norm_w + lH, m->attn_norm_s + lH / gs, t, H, gs,
-                                   m->rms_eps, 0, st),
+                                   m->rms_eps, st),
                  "rmsnorm");
         // :506-528 q, k, v in one GEMV launch
         GemvArgs g = gemv1(t, H, gs);
@@ -540,7 +540,7 @@ int q3vl_decode_step(const q3vl_text_model *m, uint16_t *k_cache, uint16_t *v_ca
         Q3VL_HIP(launch_gemv(g, true, &grid, st), "o gemv");
         // :611-661 pre-MLP RMSNorm, gate/up + swiglu, down, residual add
         Q3VL_HIP(launch_rmsnorm_i8(x, m->mlp_norm_w + lH, m->mlp_norm_s + lH / gs, t, H, gs,
-                                   m->rms_eps, 0, st),
+                                   m->rms_eps, st),
                  "rmsnorm");
         g = gemv1(t, H, gs);
         g.nseg = 2;
@@ -555,7 +555,7 @@ int q3vl_decode_step(const q3vl_text_model *m, uint16_t *k_cache, uint16_t *v_ca
         Q3VL_HIP(launch_gemv(g, true, &grid, st), "down gemv");
     }
     // :693-705 final RMSNorm (in place), tied classifier, greedy_decode
-    Q3VL_HIP(launch_rmsnorm_i8(x, m->final_norm_w, m->final_norm_s, xf, H, gs, m->rms_eps, 1, st),
+    Q3VL_HIP(launch_rmsnorm_i8(x, m->final_norm_w, m->final_norm_s, xf, H, gs, m->rms_eps, st),
              "final rmsnorm");
     GemvArgs g = gemv1(xf, H, gs);
     g.nseg = 1;

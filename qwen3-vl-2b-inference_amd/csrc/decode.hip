@@ -1,13 +1,13 @@
 // decode.hip -- support kernels of the text decode step that calls the int8
 // path (model/src/forward.cpp:458-720), gfx950.
 //
-// Numerics follow the reference where its order is explicit (RoPE fmas,
-// exp256_ps, the 8-lane attention dot products, fp16 KV stores) and the fixed
-// orders of the CPU oracle where the reference leaves them to the compiler
-// (RMS sum of squares). Attention normalizes with the exact global maximum
-// (as the reference's softmax does) so exp256 sees the same arguments; only
-// the softmax sum and the value-weighted sum are accumulated in a different
-// (parallel) order.
+// Every floating-point step follows the reference's order, including the
+// orders its compiler picks for `omp simd` reductions on 8-wide AVX2: the
+// RMS sums of squares and the scores of the last partial block of 8
+// positions use 8 FMA lane chains folded left to right, the softmax sums 8
+// float lanes then adds them in double, and the value-weighted sum is one
+// FMA chain over positions per output element. The decode step is therefore
+// bit-exact with the CPU oracle in its fp16-cache mode.
 #include <float.h>
 
 #include "q3vl_device.hpp"
@@ -38,18 +38,66 @@ __device__ __forceinline__ float exp256(float x) {
 }
 
 __device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+// fp32 -> fp16 bits, round to nearest even, computed on the integer image.
+// A plain (_Float16) conversion lets the compiler fuse it with the fmaf that
+// produced the value (v_fma_mixlo_f16 rounds the exact result once, straight
+// to fp16), which differs from the reference's fp32 result rounded to fp16
+// whenever that result lies exactly halfway between two fp16 values.
 __device__ __forceinline__ uint16_t f2h(float f) {
-    return __builtin_bit_cast(uint16_t, (_Float16)f);  // round to nearest even
+    const uint32_t x = __float_as_uint(f);
+    const uint32_t sign = (x >> 16) & 0x8000u;
+    const uint32_t ax = x & 0x7FFFFFFFu;
+    if (ax >= 0x7F800000u) return (uint16_t)(sign | (ax > 0x7F800000u ? 0x7E00u : 0x7C00u));
+    if (ax >= 0x477FF000u) return (uint16_t)(sign | 0x7C00u);  // rounds past 65504
+    if (ax < 0x33000000u) return (uint16_t)sign;                // at most 2^-25: zero
+    uint32_t r, rem, half;
+    if (ax < 0x38800000u) {  // fp16 subnormal: keep the bits above 2^-24
+        const uint32_t shift = 126u - (ax >> 23);  // 14..24
+        const uint32_t m = (ax & 0x7FFFFFu) | 0x800000u;
+        r = m >> shift;
+        rem = m & ((1u << shift) - 1u);
+        half = 1u << (shift - 1u);
+    } else {                 // normal: rebias the exponent, drop 13 mantissa bits
+        r = (ax >> 13) - (112u << 10);
+        rem = ax & 0x1FFFu;
+        half = 0x1000u;
+    }
+    r += (rem > half || (rem == half && (r & 1u))) ? 1u : 0u;
+    return (uint16_t)(sign | r);
 }
 
-// Sum of squares of a 128-vector held as (lo = x[lane], hi = x[lane+64]) by
-// one wave, in the oracle's fixed order: 128 one-element chains, then the
-// binary tree p[c] += p[c+w], w = 64..1.
-__device__ __forceinline__ float wave_sumsq128(float lo, float hi) {
-    float v = fmaf(lo, lo, 0.0f) + fmaf(hi, hi, 0.0f);
+__device__ __forceinline__ float readlane_f(float v, int lane) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
+// Left-to-right fold of the 8 lane accumulators held by lanes 0..7:
+// ((c0 + c1) + c2) + ... + c7; wave-uniform result.
+__device__ __forceinline__ float fold8_lanes(float c) {
+    float s = readlane_f(c, 0);
 #pragma unroll
-    for (int w = 32; w >= 1; w >>= 1) v = v + __shfl_down(v, w);
-    return __shfl(v, 0);
+    for (int l = 1; l < 8; ++l) s = s + readlane_f(c, l);
+    return s;
+}
+
+// Sum of squares of a 128-vector held by one wave as (lo = x[lane],
+// hi = x[lane + 64]) in the reference's order (text_layer.cpp:247-250 as
+// compiled): chain c = lane & 7 takes x[c], x[c+8], ..., x[c+120] with one
+// FMA each -- lo of lanes c, c+8, ..., c+56, then hi of the same lanes --
+// and the 8 chains are folded left to right.
+__device__ __forceinline__ float wave_sumsq128(float lo, float hi) {
+    const int c = __lane_id() & 7;
+    float acc = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const float v = __shfl(lo, c + 8 * k);
+        acc = fmaf(v, v, acc);
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const float v = __shfl(hi, c + 8 * k);
+        acc = fmaf(v, v, acc);
+    }
+    return fold8_lanes(acc);
 }
 
 // layers/src/text_layer.cpp:240-270 (int8 group weight, in place) on one
@@ -77,38 +125,32 @@ __global__ __launch_bounds__(256) void embed_kernel(const int8_t *w, const float
 }
 
 // ----------------------------------------------------------------- RMS norm
-// One block of 256 threads per row. mode 0: rms_norm (text_layer.cpp:
-// 110-147), inv = (float)(1/sqrt(double(ss/n + eps))); mode 1:
-// rms_norm_inplace (text_layer.cpp:234-270), inv = 1.0f/sqrtf(ss/n + eps).
-// out = w * ((s_g * inv) * x). Sum of squares in the oracle's fixed order:
-// 256 chains (chain c: x[c], x[c+256], ...), then p[c] += p[c+w], w=128..1.
+// One block of 256 threads per row of n <= RMS_MAX (n % 8 == 0, n % gs == 0).
+// rms_norm (text_layer.cpp:110-147) and rms_norm_inplace (text_layer.cpp:
+// 234-270) with int8 group weights: ss in the 8-lane order (lanes 0..7 of
+// wave 0 run the chains over the row staged in LDS), inv = 1 / sqrt(ss/n +
+// eps) rounded to fp32 -- both functions give the same value: sqrtf of the
+// fp32 argument, then an fp32 reciprocal or a double one rounded to fp32,
+// which agree -- and out = w * ((s_g * inv) * x).
+constexpr int RMS_MAX = 8192;
+
 __global__ __launch_bounds__(256) void rmsnorm_i8_kernel(const float *x, const int8_t *w,
                                                          const float *ws, float *out, int n,
-                                                         int gs, float eps, int mode) {
-    __shared__ float p[256];
+                                                         int gs, float eps) {
+    __shared__ float xs[RMS_MAX];
     __shared__ float s_inv;
-    const int c = threadIdx.x;
-    const int C = n < 256 ? n : 256;
-    float v = 0.0f;
-    if (c < C)
-        for (int j = c; j < n; j += C) v = fmaf(x[j], x[j], v);
-    p[c] = v;
+    for (int j = threadIdx.x; j < n; j += 256) xs[j] = x[j];
     __syncthreads();
-    for (int wdt = C / 2; wdt >= 64; wdt >>= 1) {
-        if (c < wdt) p[c] = p[c] + p[c + wdt];
-        __syncthreads();
-    }
-    if (c < 64) {
-        float t = p[c];
-        for (int wdt = (C / 2 < 32 ? C / 2 : 32); wdt >= 1; wdt >>= 1) t = t + __shfl_down(t, wdt);
-        if (c == 0) {
-            const float arg = t * (1.0f / (float)n) + eps;
-            s_inv = mode == 0 ? (float)(1.0 / __builtin_sqrt((double)arg)) : rcp_rn(sqrt_rn(arg));
-        }
+    if (threadIdx.x < 64) {
+        float acc = 0.0f;
+        if (threadIdx.x < 8)
+            for (int j = threadIdx.x; j < n; j += 8) acc = fmaf(xs[j], xs[j], acc);
+        const float ss = fold8_lanes(acc);
+        if (threadIdx.x == 0) s_inv = rcp_rn(sqrt_rn(ss * rcp_rn((float)n) + eps));
     }
     __syncthreads();
     const float inv = s_inv;
-    for (int j = c; j < n; j += 256) out[j] = (float)w[j] * ((ws[j / gs] * inv) * x[j]);
+    for (int j = threadIdx.x; j < n; j += 256) out[j] = (float)w[j] * ((ws[j / gs] * inv) * xs[j]);
 }
 
 // --------------------------------------------------------------- attention
@@ -117,7 +159,8 @@ __global__ __launch_bounds__(256) void rmsnorm_i8_kernel(const float *x, const i
 // forward.cpp:531-545); the chunk holding `pos` also normalizes + rotates the
 // new key and stores it and the new value as fp16 at pos (forward.cpp:
 // 548-562). Scores follow text_layer.cpp:598-620 exactly: 8 FMA lane chains
-// over the head dimension, the fixed tree, times 1/sqrt(hd).
+// over the head dimension, the fixed tree (the left-to-right fold for the
+// positions of the last partial block of 8), times 1/sqrt(hd).
 constexpr int ATT_CH = 64;
 constexpr int ATT_HD = 128;
 constexpr int ATT_KSTR = ATT_HD + 8;  // halves per LDS key row (272 B: bank-spread)
@@ -186,7 +229,15 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(AttnArgs a) {
                 cc[l] = fmaf(qsh[wid][i + l], h2f(hb), cc[l]);
             }
         }
-        score = tree8(cc[0], cc[1], cc[2], cc[3], cc[4], cc[5], cc[6], cc[7]) * a.inv_sqrt_d;
+        float dot;
+        if (t >= (pos & ~7)) {  // text_layer.cpp:626-633: lanes folded left to right
+            dot = cc[0];
+#pragma unroll
+            for (int l = 1; l < 8; ++l) dot = dot + cc[l];
+        } else {                // text_layer.cpp:598-620: the fixed tree
+            dot = tree8(cc[0], cc[1], cc[2], cc[3], cc[4], cc[5], cc[6], cc[7]);
+        }
+        score = dot * a.inv_sqrt_d;
         a.scores[(size_t)h * a.max_seq + t] = score;
     }
     float m = score;
@@ -195,61 +246,146 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(AttnArgs a) {
     if (lane == 0) a.cmax[h * a.max_chunks + ch] = m;
 }
 
-// B: per (query head, chunk): e_t = exp256(s_t - M) with the head's exact
-// maximum M, chunk sum of e_t and partial value sums sum_t e_t * v_t[d].
-__global__ __launch_bounds__(ATT_HD) void attn_pv_kernel(AttnArgs a) {
-    __shared__ float e[ATT_CH];
-    __shared__ float red[2];
-    const int h = blockIdx.x, ch = blockIdx.y;
-    const int pos = *a.pos;
-    const int n = pos + 1;
-    const int t0 = ch * ATT_CH;
-    if (t0 >= n) return;
-    const int nch = (n + ATT_CH - 1) / ATT_CH;
-    const int d = threadIdx.x;
-    const int kvm = a.heads / a.kv_heads;
-    // exact maximum over the head's chunk maxima
-    float M = -INFINITY;
-    for (int c = 0; c < nch; ++c) M = fmaxf(M, a.cmax[h * a.max_chunks + c]);
-    const int rows = min(ATT_CH, n - t0);
-    if (d < ATT_CH) {
-        float ev = 0.0f;
-        if (d < rows) {
-            const float sc = a.scores[(size_t)h * a.max_seq + t0 + d];
-            ev = sc > -INFINITY ? exp256(sc - M) : 0.0f;  // text_layer.cpp:486-493
-        }
-        e[d] = ev;
-        float sum = ev;
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
-        if (d == 0) red[0] = sum;
-    }
-    __syncthreads();
-    const uint16_t *vc = a.v_cache + (size_t)a.layer * a.kv_heads * a.max_seq * ATT_HD +
-                         ((size_t)(h / kvm) * a.max_seq + t0) * ATT_HD;
-    float o = 0.0f;
-#pragma unroll 8
-    for (int r = 0; r < rows; ++r) o = fmaf(e[r], h2f(vc[(size_t)r * ATT_HD + d]), o);
-    a.po[((size_t)h * a.max_chunks + ch) * ATT_HD + d] = o;
-    if (d == 0) a.psum[h * a.max_chunks + ch] = red[0];
-}
+// B: softmax (text_layer.cpp:436-535) and the value-weighted sum
+// (text_layer.cpp:655-710) in the reference's order. Block (kv head kvh,
+// slice db) serves the kvm query heads of kvh and the PV_D output dims
+// [db*PV_D, db*PV_D + PV_D). Per head:
+//   M = max of the scores (exact: the scores kernel's chunk maxima),
+//   e_t = exp256(s_t - M) (0 for s_t = -inf),
+//   sum = double(l_0) + ... + double(l_7) + e_nb + ... + e_pos (in double),
+//     l_j = sequential fp32 sum of e_t over t = j (mod 8), t < nb = n/8*8,
+//   p_t = e_t * (float)(1/sum)   (all zero if M or sum is not finite/positive),
+//   out[d] = fma chain over t = 0..pos of p_t * v_t[d].
+// p lives in LDS; V passes through LDS in chunks of PV_TC positions stored
+// transposed ([d][t], two positions per dword) so a lane reads 8 positions
+// of its dim with one 16-byte load; the chunk after the current one is
+// already in flight while the chains run.
+constexpr int PV_D = 32;
+constexpr int PV_TC = 1024;
+constexpr int PV_THREADS = 256;
+constexpr int PV_RS = PV_TC / 2 + 4;                 // dwords per LDS row of vt
+constexpr int PV_ITEMS = (PV_TC / 2) * (PV_D / 8) / PV_THREADS;  // position pairs x 8-dim segments
 
-// C: per query head: sum = sum_c psum_c (double, chunk order), inv = 1/sum as
-// in text_layer.cpp:522, out[d] = (sum_c po_c[d]) * inv. A head whose sum is
-// not positive and finite gets zeros (text_layer.cpp:514-517).
-__global__ __launch_bounds__(ATT_HD) void attn_combine_kernel(AttnArgs a) {
-    const int h = blockIdx.x, d = threadIdx.x;
-    const int pos = *a.pos;
-    const int nch = (pos + 1 + ATT_CH - 1) / ATT_CH;
-    double sum = 0.0;
-    float o = 0.0f;
-    for (int c = 0; c < nch; ++c) {
-        sum += (double)a.psum[h * a.max_chunks + c];
-        o += a.po[((size_t)h * a.max_chunks + c) * ATT_HD + d];
+__global__ __launch_bounds__(PV_THREADS) void attn_softmax_pv_kernel(AttnArgs a) {
+    extern __shared__ float smem[];
+    uint32_t *vt = reinterpret_cast<uint32_t *>(smem);  // [PV_D][PV_RS]
+    float *p = smem + PV_D * PV_RS;                     // [kvm][max_seq]
+    __shared__ float hinfo[4], hinv[4];  // per head: M, 1/sum
+    const int kvh = blockIdx.x, db = blockIdx.y;
+    const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63;
+    const int kvm = a.heads / a.kv_heads;
+    const int n = *a.pos + 1;
+    const int nb = n & ~7;
+    const uint16_t *vc = a.v_cache + ((size_t)a.layer * a.kv_heads + kvh) * a.max_seq * ATT_HD +
+                         db * PV_D;
+
+    // V chunk loads: item i -> segment (8 dims) sg, position pair pp; two
+    // 16-byte rows (t = 2pp, 2pp+1) per item, zero past the context.
+    u32x4 r0[PV_ITEMS], r1[PV_ITEMS];
+    auto load_chunk = [&](int t0) {
+#pragma unroll
+        for (int it = 0; it < PV_ITEMS; ++it) {
+            const int item = it * PV_THREADS + tid;
+            const int sg = item / (PV_TC / 2), pp = item % (PV_TC / 2);
+            const int t = t0 + 2 * pp;
+            const int ta = min(t, n - 1), tb = min(t + 1, n - 1);
+            r0[it] = *reinterpret_cast<const u32x4 *>(vc + (size_t)ta * ATT_HD + sg * 8);
+            r1[it] = *reinterpret_cast<const u32x4 *>(vc + (size_t)tb * ATT_HD + sg * 8);
+        }
+    };
+    auto store_chunk = [&]() {
+#pragma unroll
+        for (int it = 0; it < PV_ITEMS; ++it) {
+            const int item = it * PV_THREADS + tid;
+            const int sg = item / (PV_TC / 2), pp = item % (PV_TC / 2);
+            const uint32_t w0[4] = {r0[it].x, r0[it].y, r0[it].z, r0[it].w};
+            const uint32_t w1[4] = {r1[it].x, r1[it].y, r1[it].z, r1[it].w};
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const uint32_t h0 = (w0[i >> 1] >> (16 * (i & 1))) & 0xFFFFu;
+                const uint32_t h1 = (w1[i >> 1] >> (16 * (i & 1))) & 0xFFFFu;
+                vt[(sg * 8 + i) * PV_RS + pp] = h0 | (h1 << 16);
+            }
+        }
+    };
+    load_chunk(0);
+
+    // maxima from the chunk maxima
+    const int nch = (n + ATT_CH - 1) / ATT_CH;
+    if (wid < kvm) {
+        const int h = kvh * kvm + wid;
+        float m = -INFINITY;
+        for (int c = lane; c < nch; c += 64) m = fmaxf(m, a.cmax[h * a.max_chunks + c]);
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+        if (lane == 0) hinfo[wid] = m;
     }
-    float r = 0.0f;
-    if (sum > 0.0 && __builtin_isfinite(sum)) r = o * (float)(1.0 / sum);
-    a.out[h * ATT_HD + d] = r;
+    lds_barrier();
+    // e_t
+    for (int hh = 0; hh < kvm; ++hh) {
+        const float M = hinfo[hh];
+        const bool fin = __builtin_isfinite(M);
+        const float *sc = a.scores + (size_t)(kvh * kvm + hh) * a.max_seq;
+        for (int t = tid; t < n; t += PV_THREADS) {
+            const float v = sc[t];
+            p[hh * a.max_seq + t] = (fin && v > -INFINITY) ? exp256(v - M) : 0.0f;
+        }
+    }
+    lds_barrier();
+    // sums and the fp32 inverse, one wave per head
+    if (wid < kvm) {
+        const float *ph = p + wid * a.max_seq;
+        float ls = 0.0f;
+        if (lane < 8)
+            for (int t = lane; t < nb; t += 8) ls = ls + ph[t];
+        double sum = 0.0;
+#pragma unroll
+        for (int l = 0; l < 8; ++l) sum += (double)readlane_f(ls, l);
+        for (int t = nb; t < n; ++t) sum += (double)ph[t];
+        const bool ok = __builtin_isfinite(hinfo[wid]) && sum > 0.0 && __builtin_isfinite(sum);
+        const float inv = ok ? (float)(1.0 / sum) : 0.0f;
+        if (lane == 0) hinv[wid] = inv;
+    }
+    lds_barrier();
+    for (int hh = 0; hh < kvm; ++hh) {
+        const float inv = hinv[hh];
+        for (int t = tid; t < n; t += PV_THREADS) p[hh * a.max_seq + t] *= inv;
+    }
+
+    // value-weighted sums
+    const int ch_d = tid % PV_D, ch_h = tid / PV_D;
+    const bool chain = ch_h < kvm;
+    float acc = 0.0f;
+    for (int t0 = 0; t0 < n; t0 += PV_TC) {
+        lds_barrier();  // vt free (previous chains done); p final
+        store_chunk();
+        lds_barrier();
+        if (t0 + PV_TC < n) load_chunk(t0 + PV_TC);
+        if (chain) {
+            const float *ph = p + ch_h * a.max_seq + t0;
+            const uint32_t *vr = vt + ch_d * PV_RS;
+            const int len = min(PV_TC, n - t0);
+            int t = 0;
+            for (; t + 8 <= len; t += 8) {
+                const u32x4 vv = *reinterpret_cast<const u32x4 *>(vr + t / 2);
+                const float4 pa = *reinterpret_cast<const float4 *>(ph + t);
+                const float4 pb = *reinterpret_cast<const float4 *>(ph + t + 4);
+                acc = fmaf(pa.x, h2f((uint16_t)vv.x), acc);
+                acc = fmaf(pa.y, h2f((uint16_t)(vv.x >> 16)), acc);
+                acc = fmaf(pa.z, h2f((uint16_t)vv.y), acc);
+                acc = fmaf(pa.w, h2f((uint16_t)(vv.y >> 16)), acc);
+                acc = fmaf(pb.x, h2f((uint16_t)vv.z), acc);
+                acc = fmaf(pb.y, h2f((uint16_t)(vv.z >> 16)), acc);
+                acc = fmaf(pb.z, h2f((uint16_t)vv.w), acc);
+                acc = fmaf(pb.w, h2f((uint16_t)(vv.w >> 16)), acc);
+            }
+            for (; t < len; ++t) {
+                const uint32_t w2 = vr[t / 2];
+                acc = fmaf(ph[t], h2f((uint16_t)(w2 >> (16 * (t & 1)))), acc);
+            }
+        }
+    }
+    if (chain) a.out[(kvh * kvm + ch_h) * ATT_HD + db * PV_D + ch_d] = acc;
 }
 
 // ------------------------------------------------------------------ launch
@@ -260,23 +396,34 @@ hipError_t launch_embed(const int8_t *w, const float *s, const int32_t *token, f
 }
 
 hipError_t launch_rmsnorm_i8(const float *x, const int8_t *w, const float *ws, float *out, int n,
-                             int gs, float eps, int mode, hipStream_t st) {
-    if (n < 2 || (n & (n - 1)) != 0 || n % gs != 0) return hipErrorInvalidValue;
-    rmsnorm_i8_kernel<<<1, 256, 0, st>>>(x, w, ws, out, n, gs, eps, mode);
+                             int gs, float eps, hipStream_t st) {
+    if (n < 8 || n > RMS_MAX || n % 8 != 0 || gs <= 0 || n % gs != 0) return hipErrorInvalidValue;
+    rmsnorm_i8_kernel<<<1, 256, 0, st>>>(x, w, ws, out, n, gs, eps);
     return hipGetLastError();
+}
+
+size_t attention_lds_bytes(int heads, int kv_heads, int max_seq) {
+    return (size_t)PV_D * PV_RS * 4 + (size_t)(heads / kv_heads) * max_seq * 4;
 }
 
 hipError_t launch_attention(const AttnArgs &a, hipStream_t st) {
     const int kvm = a.heads / a.kv_heads;
-    if (a.head_dim != ATT_HD || a.heads % a.kv_heads != 0 || kvm < 1 || kvm > 3)
+    if (a.head_dim != ATT_HD || a.heads % a.kv_heads != 0 || kvm < 1 || kvm > 3 ||
+        a.max_seq % 8 != 0)
         return hipErrorInvalidValue;
+    const size_t lds = attention_lds_bytes(a.heads, a.kv_heads, a.max_seq);
+    if (lds > kAttnMaxLds) return hipErrorInvalidValue;
     attn_scores_kernel<<<dim3(a.kv_heads, a.max_chunks), 64 * (kvm + 1), 0, st>>>(a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    attn_pv_kernel<<<dim3(a.heads, a.max_chunks), ATT_HD, 0, st>>>(a);
-    e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    attn_combine_kernel<<<a.heads, ATT_HD, 0, st>>>(a);
+    static int lds_set = 0;  // raise the dynamic LDS limit once per process
+    if (!lds_set) {
+        e = hipFuncSetAttribute(reinterpret_cast<const void *>(&attn_softmax_pv_kernel),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)kAttnMaxLds);
+        if (e != hipSuccess) return e;
+        lds_set = 1;
+    }
+    attn_softmax_pv_kernel<<<dim3(a.kv_heads, ATT_HD / PV_D), PV_THREADS, lds, st>>>(a);
     return hipGetLastError();
 }
 

@@ -34,13 +34,6 @@ constexpr int A_STAGE = BM * BK * 2;  // bytes
 constexpr int B_STAGE = BN * BK;      // bytes
 constexpr int SC_STAGE = 2 * (BM + BN) * 4;  // up to 2 groups of a_s and w_s
 
-__device__ __forceinline__ float silu_mul_g(float gv, float uv) {
-    const float e = (float)::exp(-(double)gv);
-    const float den = 1.0f + e;
-    const float sl = (float)((double)gv / (double)den);
-    return sl * uv;
-}
-
 // 4 bytes (already xor 0x80) -> 4 fp16 values in two dwords.
 __device__ __forceinline__ void widen4(uint32_t x, uint32_t &lo, uint32_t &hi) {
     const uint32_t e = 0x64646464u;
@@ -283,7 +276,7 @@ __global__ __launch_bounds__(256, 2) void gemm_i8_kernel(GemmArgs a) {
             if (SWIGLU) {
                 const int ncol = n0 + wn * 32 + l32;
                 if (ncol < N)
-                    a.C[(size_t)mrow * N + ncol] = silu_mul_g(out[mt][0][e], out[mt][1][e]);
+                    a.C[(size_t)mrow * N + ncol] = silu_mul(out[mt][0][e], out[mt][1][e]);
             } else {
 #pragma unroll
                 for (int nt = 0; nt < 2; ++nt) {

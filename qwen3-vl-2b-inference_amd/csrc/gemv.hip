@@ -32,25 +32,6 @@ constexpr int GEMV_R = 8;          // weight rows per tile
 constexpr int GEMV_MAX_THREADS = 512;  // => K <= 8192 on this path
 constexpr int GEMV_MAX_GRID = 8192;    // the C ABI reserves this many argmax partials
 
-// SwiGLU epilogue, layers/src/text_layer.cpp:428-433:
-// silu = g / (1 + expf(-g)); h = silu * u. exp is evaluated in double and
-// rounded once (a correctly rounded expf except for halfway-close cases);
-// the division is correctly rounded as in the fp32 reference.
-__device__ __forceinline__ float silu_mul(float gv, float uv) {
-    const float e = (float)::exp(-(double)gv);
-    const float den = 1.0f + e;
-    const float sl = (float)((double)gv / (double)den);
-    return sl * uv;
-}
-
-// Workgroup barrier that orders LDS only: global loads stay in flight across
-// it (a full __syncthreads() waits for every outstanding global access).
-__device__ __forceinline__ void lds_barrier() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
 // Row stride (in words) of the per-row group buffers: a multiple of 4 whose
 // quarter is odd, so 16 lanes reading 16 bytes each at consecutive rows hit
 // distinct LDS banks.

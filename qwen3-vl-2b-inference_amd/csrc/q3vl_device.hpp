@@ -40,6 +40,63 @@ Q3VL_INLINE int32_t quant_cvt(float p) {
 Q3VL_INLINE float sqrt_rn(float x) { return (float)__builtin_sqrt((double)x); }
 Q3VL_INLINE float rcp_rn(float x) { return (float)(1.0 / (double)x); }
 
+// expf as the reference's host libm computes it (glibc >= 2.27 uses the
+// ARM optimized-routines expf by Szabolcs Nagy; on x86-64 CPUs with FMA the
+// ifunc selects the build of it compiled with FMA contraction). With N = 32:
+//   x*N/ln2 = k + r (k rounded to nearest via the 1.5*2^52 shift),
+//   exp(x) = 2^(k/N) * (1 + C2 r + C1 r^2 + C0 r^3) evaluated in double,
+// every multiply that feeds an add fused into an fma, as the compiler does.
+// kExp2Tab32[i] = bits(double nearest 2^(i/32)) - (i << 47); adding k << 47
+// to an entry applies 2^floor(k/32). Rounded once to fp32 at the end. This
+// equals the host's expf on every one of the 2^32 inputs (checked
+// exhaustively on the CPU against glibc 2.35's expf).
+static __constant__ uint64_t kExp2Tab32[32] = {
+    0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
+    0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
+    0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
+    0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
+    0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,
+    0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
+    0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
+    0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull};
+
+Q3VL_INLINE float expf_host(float x) {
+    if (x != x) return x + x;
+    if (x > 0x1.62e42ep6f) return __builtin_inff();
+    if (x < -0x1.9fe368p6f) return 0.0f;
+    const double inv_ln2_n = 0x1.71547652b82fep+0 * 32, shift = 0x1.8p+52;
+    const double c0 = 0x1.c6af84b912394p-5 / (32.0 * 32.0 * 32.0);
+    const double c1 = 0x1.ebfce50fac4f3p-3 / (32.0 * 32.0);
+    const double c2 = 0x1.62e42ff0c52d6p-1 / 32.0;
+    const double xd = (double)x;
+    double kd = __builtin_fma(inv_ln2_n, xd, shift);
+    const uint64_t ki = __builtin_bit_cast(uint64_t, kd);
+    kd = kd - shift;
+    const double r = __builtin_fma(inv_ln2_n, xd, -kd);
+    const double s = __builtin_bit_cast(double, kExp2Tab32[ki & 31] + (ki << 47));
+    const double z = __builtin_fma(c0, r, c1);
+    const double r2 = r * r;
+    const double y = __builtin_fma(c2, r, 1.0);
+    return (float)(__builtin_fma(z, r2, y) * s);
+}
+
+// SwiGLU element, layers/src/text_layer.cpp:428-433: silu = g / (1 + expf(-g)),
+// h = silu * u; the fp32 division is correctly rounded (double quotient
+// rounded once: innocuous, 53 >= 2*24+2).
+Q3VL_INLINE float silu_mul(float gv, float uv) {
+    const float den = 1.0f + expf_host(-gv);
+    const float sl = (float)((double)gv / (double)den);
+    return sl * uv;
+}
+
+// Workgroup barrier that orders LDS only: global loads stay in flight across
+// it (a full __syncthreads() waits for every outstanding global access).
+Q3VL_INLINE void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // Group scale from the 16 per-lane partial sums of squares of one group
 // (i8:148-152): the caller passes the sum tree already reduced; this applies
 // rms = sqrt(sumsq/gs + 1e-6), s = rms * fp32(1/127).

@@ -71,18 +71,22 @@ struct AttnArgs {
     const float *rope_cos, *rope_sin;       // [max_seq, hd/2]
     uint16_t *k_cache, *v_cache;            // fp16 [layers, kv_heads, max_seq, hd]
     const int32_t *pos;                     // device: position of the new token
-    float *scores, *cmax, *psum, *po;       // scratch
+    float *scores, *cmax;                   // scratch [heads, max_seq], [heads, max_chunks]
     float *out;                             // [heads*hd]
     int layer, heads, kv_heads, head_dim, max_seq, max_chunks, gs;
     float eps, inv_sqrt_d;
 };
 hipError_t launch_embed(const int8_t *w, const float *s, const int32_t *token, float *x, int H,
                         int gs, hipStream_t st);
-// mode 0: rms_norm (fp64 inverse root); mode 1: rms_norm_inplace (fp32)
+// rms_norm / rms_norm_inplace with an int8 group weight (same result), one
+// row of n <= 8192, n % 8 == 0.
 hipError_t launch_rmsnorm_i8(const float *x, const int8_t *w, const float *ws, float *out, int n,
-                             int gs, float eps, int mode, hipStream_t st);
+                             int gs, float eps, hipStream_t st);
 hipError_t launch_attention(const AttnArgs &a, hipStream_t st);
-constexpr int kAttnChunk = 64;  // positions per attention work chunk
+constexpr int kAttnChunk = 64;  // positions per attention score chunk
+// LDS the softmax/value kernel needs; at most kAttnMaxLds.
+size_t attention_lds_bytes(int heads, int kv_heads, int max_seq);
+constexpr size_t kAttnMaxLds = 160 * 1024 - 256;
 
 // ---------------------------------------------------------- GEMM (MFMA)
 struct GemmArgs {

@@ -82,6 +82,58 @@ class Oracle:
         self.lib.orc_swiglu(_p(g), _p(u), g.size)
         return g
 
+    # ---- decode step
+    def decode_step(self, dims, arrays, k_cache, v_cache, token, pos, kv_fp16=True):
+        """Returns (next_id, logits); updates the caches at pos in place."""
+        L = self.lib
+        L.orc_decode_step.restype = ctypes.c_int32
+        L.orc_decode_step.argtypes = [_vp, _vp, _vp, ctypes.c_int, ctypes.c_int32, _sz, _vp]
+        st = _model_struct(dims, arrays)
+        logits = np.zeros(dims["vocab"], np.float32)
+        nid = L.orc_decode_step(ctypes.byref(st), _p(k_cache), _p(v_cache), int(kv_fp16), token,
+                                pos, _p(logits))
+        return int(nid), logits
+
+    def rms_norm_i8(self, x, w, ws, gs, eps):
+        L = self.lib
+        L.orc_rms_norm_i8.argtypes = [_vp, _vp, _vp, _sz, _sz, ctypes.c_float, _vp]
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.zeros_like(x)
+        L.orc_rms_norm_i8(_p(x), _p(w), _p(ws), x.size, gs, eps, _p(out))
+        return out
+
+    def rms_norm_inplace_i8(self, x, w, ws, gs, eps, batches):
+        L = self.lib
+        L.orc_rms_norm_inplace_i8.argtypes = [_vp, _vp, _vp, _sz, _sz, ctypes.c_float, _sz]
+        x = np.array(x, np.float32, copy=True)
+        L.orc_rms_norm_inplace_i8(_p(x), _p(w), _p(ws), x.size // batches, gs, eps, batches)
+        return x
+
+    def rope(self, x, cos_row, sin_row, heads, hd):
+        L = self.lib
+        L.orc_rope.argtypes = [_vp, _vp, _vp, _sz, _sz]
+        x = np.array(x, np.float32, copy=True)
+        L.orc_rope(_p(x), _p(np.ascontiguousarray(cos_row)), _p(np.ascontiguousarray(sin_row)),
+                   heads, hd)
+        return x
+
+    def softmax(self, x):
+        L = self.lib
+        L.orc_softmax.argtypes = [_vp, _sz]
+        x = np.array(x, np.float32, copy=True)
+        L.orc_softmax(_p(x), x.size)
+        return x
+
+    def attention(self, q, kc, vc, heads, kv_heads, hd, max_seq, pos):
+        L = self.lib
+        L.orc_attention.argtypes = [_vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _vp, _vp]
+        att = np.zeros(pos + 1, np.float32)
+        out = np.zeros(heads * hd, np.float32)
+        L.orc_attention(_p(np.ascontiguousarray(q, np.float32)), _p(np.ascontiguousarray(kc, np.float32)),
+                        _p(np.ascontiguousarray(vc, np.float32)), heads, kv_heads, hd, max_seq, pos,
+                        _p(att), _p(out))
+        return out
+
     def argmax_rows(self, logits):
         x = np.ascontiguousarray(logits, np.float32)
         if x.ndim == 1:
@@ -89,6 +141,20 @@ class Oracle:
         ids = np.zeros(x.shape[0], np.int32)
         self.lib.orc_argmax_rows(_p(x), x.shape[0], x.shape[1], _p(ids))
         return ids
+
+
+def _model_struct(dims, arrays):
+    """orc_model / ref_model_desc over numpy arrays (same layout as the C ABI's
+    q3vl_text_model); keeps the arrays alive on the returned struct."""
+    import sys as _sys
+    pkg = os.path.join(ROOT, "qwen3-vl-2b-inference_amd")
+    if pkg not in _sys.path:
+        _sys.path.insert(0, pkg)
+    from q3vl_int8.model import make_struct
+    arrs = {k: np.ascontiguousarray(v) for k, v in arrays.items()}
+    st = make_struct(dims, lambda n: arrs[n].ctypes.data)
+    st._keep = arrs
+    return st
 
 
 class Reference:
@@ -119,3 +185,67 @@ class Reference:
         u = np.ascontiguousarray(up, np.float32)
         self.lib.ref_swiglu(_p(g), _p(u), g.size)
         return g
+
+    def rms_norm_i8(self, x, w, ws, gs, eps):
+        L = self.lib
+        L.ref_rms_norm_i8.argtypes = [_vp, _vp, _vp, _sz, _sz, ctypes.c_float, _vp]
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.zeros_like(x)
+        L.ref_rms_norm_i8(_p(x), _p(w), _p(ws), x.size, gs, eps, _p(out))
+        return out
+
+    def rms_norm_inplace_i8(self, x, w, ws, gs, eps, batches):
+        L = self.lib
+        L.ref_rms_norm_inplace_i8.argtypes = [_vp, _vp, _vp, _sz, _sz, ctypes.c_float, _sz]
+        x = np.array(x, np.float32, copy=True)
+        L.ref_rms_norm_inplace_i8(_p(x), _p(w), _p(ws), x.size // batches, gs, eps, batches)
+        return x
+
+    def rope(self, x, cos_t, sin_t, heads, hd, pos):
+        L = self.lib
+        L.ref_rope.argtypes = [_vp, _vp, _vp, _sz, ctypes.c_int, ctypes.c_int, ctypes.c_int]
+        x = np.array(x, np.float32, copy=True)
+        L.ref_rope(_p(x), _p(np.ascontiguousarray(cos_t)), _p(np.ascontiguousarray(sin_t)),
+                   cos_t.shape[0], heads, hd, pos)
+        return x
+
+    def softmax(self, x):
+        L = self.lib
+        L.ref_softmax.argtypes = [_vp, _sz]
+        x = np.array(x, np.float32, copy=True)
+        L.ref_softmax(_p(x), x.size)
+        return x
+
+    def attention(self, q, kc, vc, heads, kv_heads, hd, max_seq, pos):
+        L = self.lib
+        L.ref_attention.argtypes = [_vp, _vp, _vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, _sz,
+                                    ctypes.c_int, _vp]
+        out = np.zeros(heads * hd, np.float32)
+        L.ref_attention(_p(np.ascontiguousarray(q, np.float32)), _p(np.ascontiguousarray(kc, np.float32)),
+                        _p(np.ascontiguousarray(vc, np.float32)), heads, kv_heads, hd, max_seq, pos,
+                        _p(out))
+        return out
+
+    def decoder(self, dims, arrays, k_cache32, v_cache32):
+        """The reference's forward_text over fp32 caches (updated in place)."""
+        L = self.lib
+        L.ref_decoder_create.restype = _vp
+        L.ref_decoder_create.argtypes = [_vp, _vp, _vp]
+        L.ref_decoder_step.argtypes = [_vp, ctypes.c_int, _sz, _vp]
+        L.ref_decoder_destroy.argtypes = [_vp]
+        st = _model_struct(dims, arrays)
+        h = L.ref_decoder_create(ctypes.byref(st), _p(k_cache32), _p(v_cache32))
+        ref = self
+
+        class _Dec:
+            def step(self_, token, pos):
+                logits = np.zeros(dims["vocab"], np.float32)
+                L.ref_decoder_step(h, int(token), pos, _p(logits))
+                return logits
+
+            def close(self_):
+                L.ref_decoder_destroy(h)
+
+        d = _Dec()
+        d._keep = (st, k_cache32, v_cache32, ref)
+        return d

@@ -56,3 +56,30 @@ def test_workspace_bytes_covers_shapes():
     big = q.workspace_bytes(512, 12288, 2048, 64)
     assert 0 < small < big
     assert big >= 512 * 2048 * 2 + 512 * 32 * 4
+
+
+def _fake_model(**over):
+    """A q3vl_text_model whose tensors are fake (aligned, non-null) addresses:
+    the decode step validates the model before touching any of them."""
+    from golden.gen import SMALL
+    from q3vl_int8 import model as qm
+    dims = dict(SMALL, **over)
+    return qm.make_struct(dims, lambda n: 0x100000)
+
+
+@pytest.mark.parametrize("over,code,text", [
+    (dict(max_seq=100), q.ERR_INVALID_ARGUMENT, "multiple of 8"),
+    (dict(head_dim=64), q.ERR_UNSUPPORTED, "head_dim 128"),
+    (dict(heads=32, kv_heads=8, hidden=4096), q.ERR_UNSUPPORTED, "heads/kv_heads"),
+    (dict(max_seq=40000), q.ERR_UNSUPPORTED, "too long"),
+    (dict(inter=1000), q.ERR_UNSUPPORTED, "[1024, 8192]"),
+])
+def test_decode_step_rejects_unsupported_models(over, code, text):
+    lib = q.lib()
+    s = _fake_model(**over)
+    lib.q3vl_decode_step.restype = ctypes.c_int
+    one = ctypes.c_void_p(0x200000)
+    rc = lib.q3vl_decode_step(ctypes.byref(s), one, one, one, one, one, None, ctypes.c_size_t(0),
+                              None)
+    assert rc == code, q.last_error()
+    assert text in q.last_error()

@@ -1,0 +1,94 @@
+"""The GPU decode step (q3vl_decode_step through the C ABI) against the
+oracle's decode step in its fp16-cache mode (oracle/decode_oracle.c, a
+restatement of model/src/forward.cpp:458-720 pinned bit for bit against the
+reference's compiled forward_text in tests/test_decode_oracle.py).
+
+Bar: logits, every K/V cache row and the greedy ids bit-exact; the step
+reads token and pos from device memory and advances both there.
+"""
+import numpy as np
+import pytest
+
+from golden.gen import QWEN3VL_2B, SMALL, make_kv_cache, make_text_model
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def dev():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from q3vl_int8 import model as qm
+    return torch, qm
+
+
+class Stepper:
+    """Device and oracle copies of one model + caches, stepped together."""
+
+    def __init__(self, dev, orc, dims, seed, ctx, token):
+        torch, qm = dev
+        self.torch, self.qm, self.orc, self.dims = torch, qm, orc, dims
+        self.m = make_text_model(seed, dims)
+        k16, v16 = make_kv_cache(seed + 1, dims, ctx)
+        self.ko, self.vo = k16.view(np.uint16).copy(), v16.view(np.uint16).copy()
+        self.model = qm.DeviceTextModel(dims, self.m)
+        self.kd = torch.from_numpy(k16.view(np.int16).copy()).cuda()
+        self.vd = torch.from_numpy(v16.view(np.int16).copy()).cuda()
+        self.tok = torch.tensor([token], dtype=torch.int32, device="cuda")
+        self.pos = torch.tensor([ctx], dtype=torch.int32, device="cuda")
+        self.logits = torch.zeros(dims["vocab"], dtype=torch.float32, device="cuda")
+        self.ws = qm.alloc_decode_workspace(self.model)
+        self.token, self.p = token, ctx
+
+    def step(self):
+        torch = self.torch
+        self.qm.decode_step(self.model, self.kd, self.vd, self.tok, self.pos, self.logits,
+                            self.ws)
+        torch.cuda.synchronize()
+        nid, lo = self.orc.decode_step(self.dims, self.m, self.ko, self.vo, self.token, self.p,
+                                       kv_fp16=True)
+        lg = self.logits.cpu().numpy()
+        tag = f"pos={self.p} token={self.token}"
+        np.testing.assert_array_equal(lg.view(np.uint32), lo.view(np.uint32), err_msg=tag)
+        np.testing.assert_array_equal(self.kd.cpu().numpy().view(np.uint16), self.ko, err_msg=tag)
+        np.testing.assert_array_equal(self.vd.cpu().numpy().view(np.uint16), self.vo, err_msg=tag)
+        assert int(self.tok.item()) == nid, tag
+        assert int(self.pos.item()) == self.p + 1, tag
+        self.token, self.p = nid, self.p + 1
+        return nid
+
+
+def test_decode_chained_steps_small(dev, orc):
+    s = Stepper(dev, orc, dict(SMALL), seed=21, ctx=100, token=7)
+    for _ in range(4):
+        s.step()
+
+
+@pytest.mark.parametrize("pos", [0, 7, 8, 63, 64, 255])
+def test_decode_edge_positions(dev, orc, pos):
+    dims = dict(SMALL, layers=1)
+    Stepper(dev, orc, dims, seed=30 + pos, ctx=pos, token=pos % 4096).step()
+
+
+@pytest.mark.parametrize("pos", [1023, 1024, 1100])
+def test_decode_context_past_one_value_chunk(dev, orc, pos):
+    """Contexts of 1024, 1025 and 1101 positions: the value-weighted sum
+    stages V through LDS in chunks of 1024 positions."""
+    dims = dict(SMALL, layers=1, max_seq=1280)
+    Stepper(dev, orc, dims, seed=40, ctx=pos, token=11).step()
+
+
+def test_decode_three_query_heads_per_kv_head(dev, orc):
+    dims = dict(SMALL, layers=1, heads=24, kv_heads=8, hidden=3072, inter=1024)
+    Stepper(dev, orc, dims, seed=50, ctx=70, token=3).step()
+
+
+def test_decode_full_config_step(dev, orc):
+    """One step of the full Qwen3-VL-2B text decoder (28 layers, vocab
+    151936) at context 1024 with random weights, the benchmarked workload."""
+    print("full-size decode step: building model", flush=True)
+    dims = dict(QWEN3VL_2B, max_seq=1088)
+    s = Stepper(dev, orc, dims, seed=60, ctx=1024, token=151000)
+    print("full-size decode step: stepping", flush=True)
+    s.step()
