@@ -319,6 +319,10 @@ int check_model(const q3vl_text_model *m) {
     const void *w16[] = {m->embed_w, m->wq, m->wk, m->wv, m->wo, m->wg, m->wu, m->wd};
     for (const void *p : w16)
         if (!aligned16(p)) return fail(Q3VL_ERR_INVALID_ARGUMENT, "weights must be 16-byte aligned");
+    const void *w8[] = {m->final_norm_w, m->attn_norm_w, m->mlp_norm_w};
+    for (const void *p : w8)
+        if (((uintptr_t)p & 7u) != 0)
+            return fail(Q3VL_ERR_INVALID_ARGUMENT, "norm weights must be 8-byte aligned");
     return Q3VL_OK;
 }
 

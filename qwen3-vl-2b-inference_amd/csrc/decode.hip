@@ -127,30 +127,74 @@ __global__ __launch_bounds__(256) void embed_kernel(const int8_t *w, const float
 // ----------------------------------------------------------------- RMS norm
 // One block of 256 threads per row of n <= RMS_MAX (n % 8 == 0, n % gs == 0).
 // rms_norm (text_layer.cpp:110-147) and rms_norm_inplace (text_layer.cpp:
-// 234-270) with int8 group weights: ss in the 8-lane order (lanes 0..7 of
-// wave 0 run the chains over the row staged in LDS), inv = 1 / sqrt(ss/n +
-// eps) rounded to fp32 -- both functions give the same value: sqrtf of the
-// fp32 argument, then an fp32 reciprocal or a double one rounded to fp32,
-// which agree -- and out = w * ((s_g * inv) * x).
+// 234-270) with int8 group weights: ss in the 8-lane order, inv = 1 /
+// sqrt(ss/n + eps) rounded to fp32 -- both functions give the same value:
+// sqrtf of the fp32 argument, then an fp32 reciprocal or a double one
+// rounded to fp32, which agree -- and out = w * ((s_g * inv) * x).
+// Thread i owns x[8i .. 8i+7] (one item; more items when n > 2048) and
+// writes them chain-major to LDS, xs[l][j] = x[l + 8j], so chain lane l
+// reads its terms four at a time.
 constexpr int RMS_MAX = 8192;
+constexpr int RMS_RS = RMS_MAX / 8 + 4;  // floats per chain row (16-byte padded)
 
 __global__ __launch_bounds__(256) void rmsnorm_i8_kernel(const float *x, const int8_t *w,
                                                          const float *ws, float *out, int n,
                                                          int gs, float eps) {
-    __shared__ float xs[RMS_MAX];
+    __shared__ __align__(16) float xs[8 * RMS_RS];
     __shared__ float s_inv;
-    for (int j = threadIdx.x; j < n; j += 256) xs[j] = x[j];
+    const int items = n >> 3;
+    for (int it = threadIdx.x; it < items; it += 256) {
+        const float4 a = reinterpret_cast<const float4 *>(x)[2 * it];
+        const float4 b = reinterpret_cast<const float4 *>(x)[2 * it + 1];
+        xs[0 * RMS_RS + it] = a.x;
+        xs[1 * RMS_RS + it] = a.y;
+        xs[2 * RMS_RS + it] = a.z;
+        xs[3 * RMS_RS + it] = a.w;
+        xs[4 * RMS_RS + it] = b.x;
+        xs[5 * RMS_RS + it] = b.y;
+        xs[6 * RMS_RS + it] = b.z;
+        xs[7 * RMS_RS + it] = b.w;
+    }
     __syncthreads();
     if (threadIdx.x < 64) {
         float acc = 0.0f;
-        if (threadIdx.x < 8)
-            for (int j = threadIdx.x; j < n; j += 8) acc = fmaf(xs[j], xs[j], acc);
+        if (threadIdx.x < 8) {
+            const float *row = xs + threadIdx.x * RMS_RS;
+            int j = 0;
+            for (; j + 32 <= items; j += 32) {
+                float4 v[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) v[u] = *reinterpret_cast<const float4 *>(row + j + 4 * u);
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    acc = fmaf(v[u].x, v[u].x, acc);
+                    acc = fmaf(v[u].y, v[u].y, acc);
+                    acc = fmaf(v[u].z, v[u].z, acc);
+                    acc = fmaf(v[u].w, v[u].w, acc);
+                }
+            }
+            for (; j < items; ++j) acc = fmaf(row[j], row[j], acc);
+        }
         const float ss = fold8_lanes(acc);
         if (threadIdx.x == 0) s_inv = rcp_rn(sqrt_rn(ss * rcp_rn((float)n) + eps));
     }
     __syncthreads();
     const float inv = s_inv;
-    for (int j = threadIdx.x; j < n; j += 256) out[j] = (float)w[j] * ((ws[j / gs] * inv) * xs[j]);
+    for (int it = threadIdx.x; it < items; it += 256) {
+        float v[8];
+#pragma unroll
+        for (int l = 0; l < 8; ++l) v[l] = xs[l * RMS_RS + it];
+        const int j0 = 8 * it;
+        const uint2 wq = *reinterpret_cast<const uint2 *>(w + j0);
+        float o[8];
+#pragma unroll
+        for (int l = 0; l < 8; ++l) {
+            const int8_t wb = (int8_t)(((l < 4 ? wq.x : wq.y) >> (8 * (l & 3))) & 0xFF);
+            o[l] = (float)wb * ((ws[(j0 + l) / gs] * inv) * v[l]);
+        }
+        reinterpret_cast<float4 *>(out)[2 * it] = make_float4(o[0], o[1], o[2], o[3]);
+        reinterpret_cast<float4 *>(out)[2 * it + 1] = make_float4(o[4], o[5], o[6], o[7]);
+    }
 }
 
 // --------------------------------------------------------------- attention
@@ -267,7 +311,7 @@ constexpr int PV_RS = PV_TC / 2 + 4;                 // dwords per LDS row of vt
 constexpr int PV_ITEMS = (PV_TC / 2) * (PV_D / 8) / PV_THREADS;  // position pairs x 8-dim segments
 
 __global__ __launch_bounds__(PV_THREADS) void attn_softmax_pv_kernel(AttnArgs a) {
-    extern __shared__ float smem[];
+    extern __shared__ __align__(16) float smem[];
     uint32_t *vt = reinterpret_cast<uint32_t *>(smem);  // [PV_D][PV_RS]
     float *p = smem + PV_D * PV_RS;                     // [kvm][max_seq]
     __shared__ float hinfo[4], hinv[4];  // per head: M, 1/sum
@@ -336,8 +380,17 @@ __global__ __launch_bounds__(PV_THREADS) void attn_softmax_pv_kernel(AttnArgs a)
     if (wid < kvm) {
         const float *ph = p + wid * a.max_seq;
         float ls = 0.0f;
-        if (lane < 8)
-            for (int t = lane; t < nb; t += 8) ls = ls + ph[t];
+        if (lane < 8) {
+            int t = lane;
+            for (; t + 8 * 16 <= nb; t += 8 * 16) {
+                float v[16];
+#pragma unroll
+                for (int u = 0; u < 16; ++u) v[u] = ph[t + 8 * u];
+#pragma unroll
+                for (int u = 0; u < 16; ++u) ls = ls + v[u];
+            }
+            for (; t < nb; t += 8) ls = ls + ph[t];
+        }
         double sum = 0.0;
 #pragma unroll
         for (int l = 0; l < 8; ++l) sum += (double)readlane_f(ls, l);
@@ -365,11 +418,9 @@ __global__ __launch_bounds__(PV_THREADS) void attn_softmax_pv_kernel(AttnArgs a)
             const float *ph = p + ch_h * a.max_seq + t0;
             const uint32_t *vr = vt + ch_d * PV_RS;
             const int len = min(PV_TC, n - t0);
-            int t = 0;
-            for (; t + 8 <= len; t += 8) {
-                const u32x4 vv = *reinterpret_cast<const u32x4 *>(vr + t / 2);
-                const float4 pa = *reinterpret_cast<const float4 *>(ph + t);
-                const float4 pb = *reinterpret_cast<const float4 *>(ph + t + 4);
+            // batches of 32 positions; the next batch's LDS reads are issued
+            // before the current batch's FMAs (every read stays below len)
+            auto fma8 = [&](const u32x4 &vv, const float4 &pa, const float4 &pb) {
                 acc = fmaf(pa.x, h2f((uint16_t)vv.x), acc);
                 acc = fmaf(pa.y, h2f((uint16_t)(vv.x >> 16)), acc);
                 acc = fmaf(pa.z, h2f((uint16_t)vv.y), acc);
@@ -378,6 +429,42 @@ __global__ __launch_bounds__(PV_THREADS) void attn_softmax_pv_kernel(AttnArgs a)
                 acc = fmaf(pb.y, h2f((uint16_t)(vv.z >> 16)), acc);
                 acc = fmaf(pb.z, h2f((uint16_t)vv.w), acc);
                 acc = fmaf(pb.w, h2f((uint16_t)(vv.w >> 16)), acc);
+            };
+            int t = 0;
+            if (len >= 32) {
+                u32x4 cv[4];
+                float4 cp[8];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    cv[u] = *reinterpret_cast<const u32x4 *>(vr + 4 * u);
+                    cp[2 * u] = *reinterpret_cast<const float4 *>(ph + 8 * u);
+                    cp[2 * u + 1] = *reinterpret_cast<const float4 *>(ph + 8 * u + 4);
+                }
+                for (; t + 32 <= len; t += 32) {
+                    // next batch, or the last in-range batch (a multiple of 8)
+                    const int tn = min(t + 32, (len - 32) & ~7);
+                    u32x4 nv[4];
+                    float4 np[8];
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        nv[u] = *reinterpret_cast<const u32x4 *>(vr + tn / 2 + 4 * u);
+                        np[2 * u] = *reinterpret_cast<const float4 *>(ph + tn + 8 * u);
+                        np[2 * u + 1] = *reinterpret_cast<const float4 *>(ph + tn + 8 * u + 4);
+                    }
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) fma8(cv[u], cp[2 * u], cp[2 * u + 1]);
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        cv[u] = nv[u];
+                        cp[2 * u] = np[2 * u];
+                        cp[2 * u + 1] = np[2 * u + 1];
+                    }
+                }
+            }
+            for (; t + 8 <= len; t += 8) {
+                const u32x4 vv = *reinterpret_cast<const u32x4 *>(vr + t / 2);
+                fma8(vv, *reinterpret_cast<const float4 *>(ph + t),
+                     *reinterpret_cast<const float4 *>(ph + t + 4));
             }
             for (; t < len; ++t) {
                 const uint32_t w2 = vr[t / 2];
