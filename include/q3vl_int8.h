@@ -42,9 +42,8 @@
  * library use its own per-device buffer, grown on demand with hipMalloc
  * (not allowed while the stream is being captured into a HIP graph; capture
  * callers pass their own workspace). A caller's workspace must be 256-byte
- * aligned and zero-filled before its first use: its first 256 bytes hold
- * completion counters that every call leaves at zero again. Calls sharing one
- * workspace must be ordered on one stream.
+ * aligned; its contents need no initialization (every call writes what it
+ * reads). Calls sharing one workspace must be ordered on one stream.
  */
 #ifndef Q3VL_INT8_H
 #define Q3VL_INT8_H
@@ -175,7 +174,7 @@ typedef struct q3vl_text_model {
 size_t q3vl_decode_workspace_bytes(const q3vl_text_model *m);
 
 /* One decode step; logits [vocab] are stored when non-NULL. No allocation
- * when `workspace` is given (zero-filled before first use, as above). */
+ * when `workspace` is given. */
 int q3vl_decode_step(const q3vl_text_model *m, uint16_t *k_cache, uint16_t *v_cache,
                      int32_t *token, int32_t *pos, float *logits, void *workspace,
                      size_t workspace_bytes, q3vl_stream stream);

@@ -55,7 +55,6 @@ bool gs_ok_gemm(size_t gs) { return gs == 32 || gs == 64 || gs == 128; }
 
 // ---- workspace layout
 struct WsLayout {
-    size_t counters = 0;                  // 256 bytes, zero between calls
     size_t parts_val = 0, parts_idx = 0;  // argmax partials
     size_t aq = 0, as = 0;                // GEMM: fp16 activations, transposed scales
     size_t logits = 0;                    // lm_head M > 8 without caller logits
@@ -67,8 +66,6 @@ WsLayout layout(size_t M, size_t N, size_t K, size_t gs) {
     WsLayout L;
     size_t off = 0;
     const size_t mm = M ? M : 1;
-    L.counters = off;
-    off += 256;
     L.parts_val = off;
     off += align256(kMaxGemvParts * mm * sizeof(float));
     L.parts_idx = off;
@@ -124,9 +121,6 @@ int resolve_ws(void *user, size_t user_bytes, size_t need, char **out) {
         void *p = nullptr;
         if (hipMalloc(&p, sz) != hipSuccess)
             return fail(Q3VL_ERR_OUT_OF_MEMORY, "workspace hipMalloc(%zu) failed", sz);
-        // The counter bytes at the head of the workspace must start at zero;
-        // every call leaves them zero again.
-        Q3VL_HIP(hipMemset(p, 0, 256), "hipMemset(workspace counters)");
         g_ws.buf[dev] = p;
         g_ws.size[dev] = sz;
     }

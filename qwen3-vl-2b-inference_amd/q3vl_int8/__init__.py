@@ -141,8 +141,7 @@ def _ws(workspace):
 
 
 def alloc_workspace(M, N, K, gs, device="cuda"):
-    """Zero-filled device workspace (its head holds counters that must start
-    at zero; every call leaves them zero)."""
+    """Device workspace for the linear entry points at shape (M, N, K)."""
     torch = _torch()
     return torch.zeros(workspace_bytes(M, N, K, gs), dtype=torch.uint8, device=device)
 
