@@ -252,7 +252,7 @@ std::unordered_map<const void *, RegEntry> g_reg;
 // ------------------------------------------------------------ decode step
 struct DecodeLayout {
     size_t lin;  // linear() scratch (argmax partials)
-    size_t x, t, q, k, v, ao, h, xf, scores, cmax;
+    size_t x, q, k, v, ao, h, scores, cmax;
     size_t total;
     int max_chunks;
 };
@@ -270,13 +270,11 @@ DecodeLayout decode_layout(const q3vl_text_model *m) {
     L.max_chunks = (int)((S + kAttnChunk - 1) / kAttnChunk);
     L.lin = take(layout(1, m->vocab, H, m->group_size).total);
     L.x = take(H * 4);
-    L.t = take(H * 4);
     L.q = take(NH * D * 4);
     L.k = take(NKV * D * 4);
     L.v = take(NKV * D * 4);
     L.ao = take(NH * D * 4);
     L.h = take(I * 4);
-    L.xf = take(H * 4);
     L.scores = take(NH * S * 4);
     L.cmax = take(NH * (size_t)L.max_chunks * 4);
     L.total = off;
@@ -482,8 +480,8 @@ int q3vl_decode_step(const q3vl_text_model *m, uint16_t *k_cache, uint16_t *v_ca
     const int D = m->head_dim, gs = m->group_size, V = m->vocab;
     const int QD = NH * D, KD = NKV * D;
     auto F = [&](size_t off) { return reinterpret_cast<float *>(w + off); };
-    float *x = F(L.x), *t = F(L.t), *q = F(L.q), *k = F(L.k), *v = F(L.v), *ao = F(L.ao);
-    float *hb = F(L.h), *xf = F(L.xf);
+    float *x = F(L.x), *q = F(L.q), *k = F(L.k), *v = F(L.v), *ao = F(L.ao);
+    float *hb = F(L.h);
     const WsLayout LL = layout(1, V, H, gs);
     float *pv = reinterpret_cast<float *>(w + L.lin + LL.parts_val);
     int32_t *pi = reinterpret_cast<int32_t *>(w + L.lin + LL.parts_idx);
@@ -512,12 +510,11 @@ int q3vl_decode_step(const q3vl_text_model *m, uint16_t *k_cache, uint16_t *v_ca
     int grid = 0;
     for (int l = 0; l < m->layers; ++l) {
         const size_t lH = (size_t)l * H, lD = (size_t)l * D;
-        // :493 pre-attention RMSNorm
-        Q3VL_HIP(launch_rmsnorm_i8(x, m->attn_norm_w + lH, m->attn_norm_s + lH / gs, t, H, gs,
-                                   m->rms_eps, st),
-                 "rmsnorm");
-        // :506-528 q, k, v in one GEMV launch
-        GemvArgs g = gemv1(t, H, gs);
+        // :493 pre-attention RMSNorm fused into the q, k, v GEMV (:506-528)
+        GemvArgs g = gemv1(x, H, gs);
+        g.norm_w = m->attn_norm_w + lH;
+        g.norm_s = m->attn_norm_s + lH / gs;
+        g.norm_eps = m->rms_eps;
         g.nseg = 3;
         g.seg[0] = {m->wq + (size_t)l * QD * H, m->sq + (size_t)l * QD * H / gs, q, nullptr, QD};
         g.seg[1] = {m->wk + (size_t)l * KD * H, m->sk + (size_t)l * KD * H / gs, k, nullptr, KD};
@@ -536,11 +533,12 @@ int q3vl_decode_step(const q3vl_text_model *m, uint16_t *k_cache, uint16_t *v_ca
         g.accumulate = 1;
         g.seg[0] = {m->wo + (size_t)l * H * QD, m->so + (size_t)l * H * QD / gs, x, nullptr, H};
         Q3VL_HIP(launch_gemv(g, true, &grid, st), "o gemv");
-        // :611-661 pre-MLP RMSNorm, gate/up + swiglu, down, residual add
-        Q3VL_HIP(launch_rmsnorm_i8(x, m->mlp_norm_w + lH, m->mlp_norm_s + lH / gs, t, H, gs,
-                                   m->rms_eps, st),
-                 "rmsnorm");
-        g = gemv1(t, H, gs);
+        // :611-661 pre-MLP RMSNorm fused into gate/up + swiglu, then down and
+        // the residual add
+        g = gemv1(x, H, gs);
+        g.norm_w = m->mlp_norm_w + lH;
+        g.norm_s = m->mlp_norm_s + lH / gs;
+        g.norm_eps = m->rms_eps;
         g.nseg = 2;
         g.mode = GEMV_SWIGLU;
         g.seg[0] = {m->wg + (size_t)l * I * H, m->sg + (size_t)l * I * H / gs, hb, nullptr, I};
@@ -552,10 +550,11 @@ int q3vl_decode_step(const q3vl_text_model *m, uint16_t *k_cache, uint16_t *v_ca
         g.seg[0] = {m->wd + (size_t)l * H * I, m->sd + (size_t)l * H * I / gs, x, nullptr, H};
         Q3VL_HIP(launch_gemv(g, true, &grid, st), "down gemv");
     }
-    // :693-705 final RMSNorm (in place), tied classifier, greedy_decode
-    Q3VL_HIP(launch_rmsnorm_i8(x, m->final_norm_w, m->final_norm_s, xf, H, gs, m->rms_eps, st),
-             "final rmsnorm");
-    GemvArgs g = gemv1(xf, H, gs);
+    // :693-705 final RMSNorm fused into the tied classifier, greedy_decode
+    GemvArgs g = gemv1(x, H, gs);
+    g.norm_w = m->final_norm_w;
+    g.norm_s = m->final_norm_s;
+    g.norm_eps = m->rms_eps;
     g.nseg = 1;
     g.mode = GEMV_ARGMAX;
     g.seg[0] = {m->embed_w, m->embed_s, logits, nullptr, V};

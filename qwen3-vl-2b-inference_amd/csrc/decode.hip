@@ -124,79 +124,6 @@ __global__ __launch_bounds__(256) void embed_kernel(const int8_t *w, const float
         x[i] = (float)w[base + i] * s[(base + i) / gs];
 }
 
-// ----------------------------------------------------------------- RMS norm
-// One block of 256 threads per row of n <= RMS_MAX (n % 8 == 0, n % gs == 0).
-// rms_norm (text_layer.cpp:110-147) and rms_norm_inplace (text_layer.cpp:
-// 234-270) with int8 group weights: ss in the 8-lane order, inv = 1 /
-// sqrt(ss/n + eps) rounded to fp32 -- both functions give the same value:
-// sqrtf of the fp32 argument, then an fp32 reciprocal or a double one
-// rounded to fp32, which agree -- and out = w * ((s_g * inv) * x).
-// Thread i owns x[8i .. 8i+7] (one item; more items when n > 2048) and
-// writes them chain-major to LDS, xs[l][j] = x[l + 8j], so chain lane l
-// reads its terms four at a time.
-constexpr int RMS_MAX = 8192;
-constexpr int RMS_RS = RMS_MAX / 8 + 4;  // floats per chain row (16-byte padded)
-
-__global__ __launch_bounds__(256) void rmsnorm_i8_kernel(const float *x, const int8_t *w,
-                                                         const float *ws, float *out, int n,
-                                                         int gs, float eps) {
-    __shared__ __align__(16) float xs[8 * RMS_RS];
-    __shared__ float s_inv;
-    const int items = n >> 3;
-    for (int it = threadIdx.x; it < items; it += 256) {
-        const float4 a = reinterpret_cast<const float4 *>(x)[2 * it];
-        const float4 b = reinterpret_cast<const float4 *>(x)[2 * it + 1];
-        xs[0 * RMS_RS + it] = a.x;
-        xs[1 * RMS_RS + it] = a.y;
-        xs[2 * RMS_RS + it] = a.z;
-        xs[3 * RMS_RS + it] = a.w;
-        xs[4 * RMS_RS + it] = b.x;
-        xs[5 * RMS_RS + it] = b.y;
-        xs[6 * RMS_RS + it] = b.z;
-        xs[7 * RMS_RS + it] = b.w;
-    }
-    __syncthreads();
-    if (threadIdx.x < 64) {
-        float acc = 0.0f;
-        if (threadIdx.x < 8) {
-            const float *row = xs + threadIdx.x * RMS_RS;
-            int j = 0;
-            for (; j + 32 <= items; j += 32) {
-                float4 v[8];
-#pragma unroll
-                for (int u = 0; u < 8; ++u) v[u] = *reinterpret_cast<const float4 *>(row + j + 4 * u);
-#pragma unroll
-                for (int u = 0; u < 8; ++u) {
-                    acc = fmaf(v[u].x, v[u].x, acc);
-                    acc = fmaf(v[u].y, v[u].y, acc);
-                    acc = fmaf(v[u].z, v[u].z, acc);
-                    acc = fmaf(v[u].w, v[u].w, acc);
-                }
-            }
-            for (; j < items; ++j) acc = fmaf(row[j], row[j], acc);
-        }
-        const float ss = fold8_lanes(acc);
-        if (threadIdx.x == 0) s_inv = rcp_rn(sqrt_rn(ss * rcp_rn((float)n) + eps));
-    }
-    __syncthreads();
-    const float inv = s_inv;
-    for (int it = threadIdx.x; it < items; it += 256) {
-        float v[8];
-#pragma unroll
-        for (int l = 0; l < 8; ++l) v[l] = xs[l * RMS_RS + it];
-        const int j0 = 8 * it;
-        const uint2 wq = *reinterpret_cast<const uint2 *>(w + j0);
-        float o[8];
-#pragma unroll
-        for (int l = 0; l < 8; ++l) {
-            const int8_t wb = (int8_t)(((l < 4 ? wq.x : wq.y) >> (8 * (l & 3))) & 0xFF);
-            o[l] = (float)wb * ((ws[(j0 + l) / gs] * inv) * v[l]);
-        }
-        reinterpret_cast<float4 *>(out)[2 * it] = make_float4(o[0], o[1], o[2], o[3]);
-        reinterpret_cast<float4 *>(out)[2 * it + 1] = make_float4(o[4], o[5], o[6], o[7]);
-    }
-}
-
 // --------------------------------------------------------------- attention
 // A: per (kv head, chunk of ATT_CH positions), one wave per query head of the
 // group. The waves normalize + rotate their query heads (q RMSNorm + RoPE,
@@ -300,61 +227,75 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(AttnArgs a) {
 //     l_j = sequential fp32 sum of e_t over t = j (mod 8), t < nb = n/8*8,
 //   p_t = e_t * (float)(1/sum)   (all zero if M or sum is not finite/positive),
 //   out[d] = fma chain over t = 0..pos of p_t * v_t[d].
-// p lives in LDS; V passes through LDS in chunks of PV_TC positions stored
-// transposed ([d][t], two positions per dword) so a lane reads 8 positions
-// of its dim with one 16-byte load; the chunk after the current one is
-// already in flight while the chains run.
-constexpr int PV_D = 32;
+// The chain is inherently sequential (one dependent FMA per position), so
+// everything else is arranged to keep it to one v_fmac_f32 per step: every
+// global load (the first V chunk, the chunk maxima, up to PV_SREG*PV_THREADS
+// scores per head) is issued at entry; V is widened to fp32 into LDS,
+// transposed ([d][t]); p is formed in LDS before the chains start; the chains
+// read 32 positions ahead. e also lives lane-major (row j holds e_j, e_{j+8},
+// ...) so the 8 summing lanes read contiguous 16-byte words.
+constexpr int PV_D = 16;
 constexpr int PV_TC = 1024;
 constexpr int PV_THREADS = 256;
-constexpr int PV_RS = PV_TC / 2 + 4;                 // dwords per LDS row of vt
-constexpr int PV_ITEMS = (PV_TC / 2) * (PV_D / 8) / PV_THREADS;  // position pairs x 8-dim segments
+constexpr int PV_RS = PV_TC + 4;                    // floats per LDS row of vt
+constexpr int PV_ITEMS = PV_TC * (PV_D / 8) / PV_THREADS;  // (position, 8-dim segment) items
+constexpr int PV_SREG = 8;                          // scores held in registers per head
+
+// Lane-major e rows hold max_seq/8 terms rounded up to a multiple of 32 (the
+// summing batch), plus 4 floats of padding against bank conflicts.
+__host__ __device__ __forceinline__ int pv_et_stride(int max_seq) {
+    return (max_seq / 8 + 31) / 32 * 32 + 4;
+}
 
 __global__ __launch_bounds__(PV_THREADS) void attn_softmax_pv_kernel(AttnArgs a) {
     extern __shared__ __align__(16) float smem[];
-    uint32_t *vt = reinterpret_cast<uint32_t *>(smem);  // [PV_D][PV_RS]
-    float *p = smem + PV_D * PV_RS;                     // [kvm][max_seq]
-    __shared__ float hinfo[4], hinv[4];  // per head: M, 1/sum
+    const int kvm = a.heads / a.kv_heads;
+    const int S = a.max_seq, ets = pv_et_stride(S);
+    float *vt = smem;                       // [PV_D][PV_RS] fp32
+    float *e = smem + PV_D * PV_RS;         // [kvm][S]: e_t, then p_t
+    float *et = e + kvm * S;                // [kvm][8][ets]
+    __shared__ float hmax[4], hinv[4];
     const int kvh = blockIdx.x, db = blockIdx.y;
     const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63;
-    const int kvm = a.heads / a.kv_heads;
     const int n = *a.pos + 1;
     const int nb = n & ~7;
-    const uint16_t *vc = a.v_cache + ((size_t)a.layer * a.kv_heads + kvh) * a.max_seq * ATT_HD +
-                         db * PV_D;
+    const uint16_t *vc = a.v_cache + ((size_t)a.layer * a.kv_heads + kvh) * S * ATT_HD + db * PV_D;
 
-    // V chunk loads: item i -> segment (8 dims) sg, position pair pp; two
-    // 16-byte rows (t = 2pp, 2pp+1) per item, zero past the context.
-    u32x4 r0[PV_ITEMS], r1[PV_ITEMS];
+    // V chunk loads: item -> (8-dim segment sg, position t), one 16-byte
+    // load each, clamped into the context.
+    u32x4 vr[PV_ITEMS];
     auto load_chunk = [&](int t0) {
 #pragma unroll
         for (int it = 0; it < PV_ITEMS; ++it) {
             const int item = it * PV_THREADS + tid;
-            const int sg = item / (PV_TC / 2), pp = item % (PV_TC / 2);
-            const int t = t0 + 2 * pp;
-            const int ta = min(t, n - 1), tb = min(t + 1, n - 1);
-            r0[it] = *reinterpret_cast<const u32x4 *>(vc + (size_t)ta * ATT_HD + sg * 8);
-            r1[it] = *reinterpret_cast<const u32x4 *>(vc + (size_t)tb * ATT_HD + sg * 8);
+            const int sg = item / PV_TC, t = t0 + item % PV_TC;
+            vr[it] = *reinterpret_cast<const u32x4 *>(vc + (size_t)min(t, n - 1) * ATT_HD + sg * 8);
         }
     };
     auto store_chunk = [&]() {
 #pragma unroll
         for (int it = 0; it < PV_ITEMS; ++it) {
             const int item = it * PV_THREADS + tid;
-            const int sg = item / (PV_TC / 2), pp = item % (PV_TC / 2);
-            const uint32_t w0[4] = {r0[it].x, r0[it].y, r0[it].z, r0[it].w};
-            const uint32_t w1[4] = {r1[it].x, r1[it].y, r1[it].z, r1[it].w};
+            const int sg = item / PV_TC, t = item % PV_TC;
+            const uint32_t w[4] = {vr[it].x, vr[it].y, vr[it].z, vr[it].w};
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const uint32_t h0 = (w0[i >> 1] >> (16 * (i & 1))) & 0xFFFFu;
-                const uint32_t h1 = (w1[i >> 1] >> (16 * (i & 1))) & 0xFFFFu;
-                vt[(sg * 8 + i) * PV_RS + pp] = h0 | (h1 << 16);
-            }
+            for (int i = 0; i < 8; ++i)
+                vt[(sg * 8 + i) * PV_RS + t] = h2f((uint16_t)(w[i >> 1] >> (16 * (i & 1))));
         }
     };
     load_chunk(0);
 
-    // maxima from the chunk maxima
+    // scores of this thread's positions t = tid + PV_THREADS*k, k < PV_SREG
+    float sreg[3][PV_SREG];
+#pragma unroll
+    for (int hh = 0; hh < 3; ++hh) {
+        if (hh < kvm) {
+            const float *sc = a.scores + (size_t)(kvh * kvm + hh) * S;
+#pragma unroll
+            for (int k = 0; k < PV_SREG; ++k) sreg[hh][k] = sc[min(tid + PV_THREADS * k, n - 1)];
+        }
+    }
+    // maxima from the chunk maxima, one wave per head
     const int nch = (n + ATT_CH - 1) / ATT_CH;
     if (wid < kvm) {
         const int h = kvh * kvm + wid;
@@ -362,114 +303,148 @@ __global__ __launch_bounds__(PV_THREADS) void attn_softmax_pv_kernel(AttnArgs a)
         for (int c = lane; c < nch; c += 64) m = fmaxf(m, a.cmax[h * a.max_chunks + c]);
 #pragma unroll
         for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
-        if (lane == 0) hinfo[wid] = m;
+        if (lane == 0) hmax[wid] = m;
     }
     lds_barrier();
-    // e_t
-    for (int hh = 0; hh < kvm; ++hh) {
-        const float M = hinfo[hh];
-        const bool fin = __builtin_isfinite(M);
-        const float *sc = a.scores + (size_t)(kvh * kvm + hh) * a.max_seq;
-        for (int t = tid; t < n; t += PV_THREADS) {
-            const float v = sc[t];
-            p[hh * a.max_seq + t] = (fin && v > -INFINITY) ? exp256(v - M) : 0.0f;
+    // e_t (text_layer.cpp:486-493, 501-509), stored both ways
+#pragma unroll
+    for (int hh = 0; hh < 3; ++hh) {
+        if (hh < kvm) {
+            const float M = hmax[hh];
+            const bool fin = __builtin_isfinite(M);
+            float *eh = e + hh * S, *eth = et + hh * 8 * ets;
+            auto put = [&](int t, float v) {
+                const float ev = (fin && v > -INFINITY) ? exp256(v - M) : 0.0f;
+                eh[t] = ev;
+                if (t < nb) eth[(t & 7) * ets + (t >> 3)] = ev;
+            };
+            // zeros after the lane sums' last term, up to a whole batch of 32
+            // per lane: adding +0 to a sum of non-negative terms is exact
+            const int zend = (nb + 255) & ~255;
+            for (int t = nb + tid; t < zend; t += PV_THREADS) eth[(t & 7) * ets + (t >> 3)] = 0.0f;
+#pragma unroll
+            for (int k = 0; k < PV_SREG; ++k) {
+                const int t = tid + PV_THREADS * k;
+                if (t < n) put(t, sreg[hh][k]);
+            }
+            const float *sc = a.scores + (size_t)(kvh * kvm + hh) * S;
+            for (int t = tid + PV_THREADS * PV_SREG; t < n; t += PV_THREADS) put(t, sc[t]);
         }
     }
+    store_chunk();  // V chunk 0 (its loads were issued at entry)
     lds_barrier();
-    // sums and the fp32 inverse, one wave per head
+    // sums and the fp32 inverse, lanes 0..7 of one wave per head
     if (wid < kvm) {
-        const float *ph = p + wid * a.max_seq;
+        const float *row = et + wid * 8 * ets + (lane & 7) * ets;
+        const int cnt = ((nb >> 3) + 31) & ~31;  // terms per lane, zero-padded
         float ls = 0.0f;
-        if (lane < 8) {
-            int t = lane;
-            for (; t + 8 * 16 <= nb; t += 8 * 16) {
-                float v[16];
+        if (lane < 8 && cnt > 0) {
+            float4 A[8], B[8];
+            auto ld = [&](float4 *D, int i) {
 #pragma unroll
-                for (int u = 0; u < 16; ++u) v[u] = ph[t + 8 * u];
+                for (int u = 0; u < 8; ++u) D[u] = *reinterpret_cast<const float4 *>(row + i + 4 * u);
+            };
+            auto add = [&](const float4 *D) {
 #pragma unroll
-                for (int u = 0; u < 16; ++u) ls = ls + v[u];
+                for (int u = 0; u < 8; ++u) {
+                    ls = ls + D[u].x;
+                    ls = ls + D[u].y;
+                    ls = ls + D[u].z;
+                    ls = ls + D[u].w;
+                }
+            };
+            ld(A, 0);
+            int i = 0;
+            for (; i + 64 <= cnt; i += 64) {
+                ld(B, i + 32);
+                __builtin_amdgcn_sched_barrier(0);
+                add(A);
+                __builtin_amdgcn_sched_barrier(0);
+                ld(A, min(i + 64, cnt - 32));
+                __builtin_amdgcn_sched_barrier(0);
+                add(B);
+                __builtin_amdgcn_sched_barrier(0);
             }
-            for (; t < nb; t += 8) ls = ls + ph[t];
+            if (i < cnt) add(A);  // one batch of 32 left
         }
         double sum = 0.0;
 #pragma unroll
         for (int l = 0; l < 8; ++l) sum += (double)readlane_f(ls, l);
-        for (int t = nb; t < n; ++t) sum += (double)ph[t];
-        const bool ok = __builtin_isfinite(hinfo[wid]) && sum > 0.0 && __builtin_isfinite(sum);
+        const float *eh = e + wid * S;
+        for (int t = nb; t < n; ++t) sum += (double)eh[t];
+        const bool ok = __builtin_isfinite(hmax[wid]) && sum > 0.0 && __builtin_isfinite(sum);
         const float inv = ok ? (float)(1.0 / sum) : 0.0f;
         if (lane == 0) hinv[wid] = inv;
     }
     lds_barrier();
+    // p_t = e_t * inv, in place (four positions per thread per pass, reads first)
     for (int hh = 0; hh < kvm; ++hh) {
         const float inv = hinv[hh];
-        for (int t = tid; t < n; t += PV_THREADS) p[hh * a.max_seq + t] *= inv;
+        float *eh = e + hh * S;
+        for (int t0 = 0; t0 < n; t0 += 4 * PV_THREADS) {
+            float v[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) v[k] = eh[min(t0 + tid + k * PV_THREADS, n - 1)];
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                if (t0 + tid + k * PV_THREADS < n) eh[t0 + tid + k * PV_THREADS] = v[k] * inv;
+        }
     }
 
-    // value-weighted sums
+    // value-weighted sums: lane (ch_h, ch_d) of wave 0 runs one chain
     const int ch_d = tid % PV_D, ch_h = tid / PV_D;
     const bool chain = ch_h < kvm;
     float acc = 0.0f;
     for (int t0 = 0; t0 < n; t0 += PV_TC) {
-        lds_barrier();  // vt free (previous chains done); p final
-        store_chunk();
-        lds_barrier();
+        if (t0 > 0) {
+            lds_barrier();  // previous chains done with vt
+            store_chunk();
+        }
+        lds_barrier();      // vt and p ready
         if (t0 + PV_TC < n) load_chunk(t0 + PV_TC);
         if (chain) {
-            const float *ph = p + ch_h * a.max_seq + t0;
-            const uint32_t *vr = vt + ch_d * PV_RS;
+            const float *ph = e + ch_h * S + t0;
+            const float *vrow = vt + ch_d * PV_RS;
             const int len = min(PV_TC, n - t0);
-            // batches of 32 positions; the next batch's LDS reads are issued
-            // before the current batch's FMAs (every read stays below len)
-            auto fma8 = [&](const u32x4 &vv, const float4 &pa, const float4 &pb) {
-                acc = fmaf(pa.x, h2f((uint16_t)vv.x), acc);
-                acc = fmaf(pa.y, h2f((uint16_t)(vv.x >> 16)), acc);
-                acc = fmaf(pa.z, h2f((uint16_t)vv.y), acc);
-                acc = fmaf(pa.w, h2f((uint16_t)(vv.y >> 16)), acc);
-                acc = fmaf(pb.x, h2f((uint16_t)vv.z), acc);
-                acc = fmaf(pb.y, h2f((uint16_t)(vv.z >> 16)), acc);
-                acc = fmaf(pb.z, h2f((uint16_t)vv.w), acc);
-                acc = fmaf(pb.w, h2f((uint16_t)(vv.w >> 16)), acc);
-            };
             int t = 0;
             if (len >= 32) {
-                u32x4 cv[4];
-                float4 cp[8];
+                // batches of 32 positions in two register sets used in turn:
+                // the next batch's LDS reads are issued before the current
+                // batch's FMAs (all reads < len), with no register copies
+                float4 Av[8], Ap[8], Bv[8], Bp[8];
+                auto ld = [&](float4 *V, float4 *P, int i) {
 #pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    cv[u] = *reinterpret_cast<const u32x4 *>(vr + 4 * u);
-                    cp[2 * u] = *reinterpret_cast<const float4 *>(ph + 8 * u);
-                    cp[2 * u + 1] = *reinterpret_cast<const float4 *>(ph + 8 * u + 4);
-                }
-                for (; t + 32 <= len; t += 32) {
-                    // next batch, or the last in-range batch (a multiple of 8)
-                    const int tn = min(t + 32, (len - 32) & ~7);
-                    u32x4 nv[4];
-                    float4 np[8];
-#pragma unroll
-                    for (int u = 0; u < 4; ++u) {
-                        nv[u] = *reinterpret_cast<const u32x4 *>(vr + tn / 2 + 4 * u);
-                        np[2 * u] = *reinterpret_cast<const float4 *>(ph + tn + 8 * u);
-                        np[2 * u + 1] = *reinterpret_cast<const float4 *>(ph + tn + 8 * u + 4);
+                    for (int u = 0; u < 8; ++u) {
+                        V[u] = *reinterpret_cast<const float4 *>(vrow + i + 4 * u);
+                        P[u] = *reinterpret_cast<const float4 *>(ph + i + 4 * u);
                     }
+                };
+                auto fma32 = [&](const float4 *V, const float4 *P) {
 #pragma unroll
-                    for (int u = 0; u < 4; ++u) fma8(cv[u], cp[2 * u], cp[2 * u + 1]);
-#pragma unroll
-                    for (int u = 0; u < 4; ++u) {
-                        cv[u] = nv[u];
-                        cp[2 * u] = np[2 * u];
-                        cp[2 * u + 1] = np[2 * u + 1];
+                    for (int u = 0; u < 8; ++u) {
+                        acc = fmaf(P[u].x, V[u].x, acc);
+                        acc = fmaf(P[u].y, V[u].y, acc);
+                        acc = fmaf(P[u].z, V[u].z, acc);
+                        acc = fmaf(P[u].w, V[u].w, acc);
                     }
+                };
+                ld(Av, Ap, 0);
+                for (; t + 64 <= len; t += 64) {
+                    ld(Bv, Bp, t + 32);
+                    __builtin_amdgcn_sched_barrier(0);
+                    fma32(Av, Ap);
+                    __builtin_amdgcn_sched_barrier(0);
+                    ld(Av, Ap, min(t + 64, (len - 32) & ~3));
+                    __builtin_amdgcn_sched_barrier(0);
+                    fma32(Bv, Bp);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                if (t + 32 <= len) {  // A holds positions t .. t+31
+                    fma32(Av, Ap);
+                    t += 32;
                 }
             }
-            for (; t + 8 <= len; t += 8) {
-                const u32x4 vv = *reinterpret_cast<const u32x4 *>(vr + t / 2);
-                fma8(vv, *reinterpret_cast<const float4 *>(ph + t),
-                     *reinterpret_cast<const float4 *>(ph + t + 4));
-            }
-            for (; t < len; ++t) {
-                const uint32_t w2 = vr[t / 2];
-                acc = fmaf(ph[t], h2f((uint16_t)(w2 >> (16 * (t & 1)))), acc);
-            }
+            for (; t < len; ++t) acc = fmaf(ph[t], vrow[t], acc);
         }
     }
     if (chain) a.out[(kvh * kvm + ch_h) * ATT_HD + db * PV_D + ch_d] = acc;
@@ -482,15 +457,9 @@ hipError_t launch_embed(const int8_t *w, const float *s, const int32_t *token, f
     return hipGetLastError();
 }
 
-hipError_t launch_rmsnorm_i8(const float *x, const int8_t *w, const float *ws, float *out, int n,
-                             int gs, float eps, hipStream_t st) {
-    if (n < 8 || n > RMS_MAX || n % 8 != 0 || gs <= 0 || n % gs != 0) return hipErrorInvalidValue;
-    rmsnorm_i8_kernel<<<1, 256, 0, st>>>(x, w, ws, out, n, gs, eps);
-    return hipGetLastError();
-}
-
 size_t attention_lds_bytes(int heads, int kv_heads, int max_seq) {
-    return (size_t)PV_D * PV_RS * 4 + (size_t)(heads / kv_heads) * max_seq * 4;
+    const size_t kvm = (size_t)(heads / kv_heads);
+    return (size_t)PV_D * PV_RS * 4 + kvm * max_seq * 4 + kvm * 8 * (size_t)pv_et_stride(max_seq) * 4;
 }
 
 hipError_t launch_attention(const AttnArgs &a, hipStream_t st) {

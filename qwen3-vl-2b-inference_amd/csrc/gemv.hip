@@ -82,6 +82,7 @@ __global__ __launch_bounds__(GEMV_MAX_THREADS) void gemv_kernel(GemvArgs a, int 
     // scale values per thread per tile: R*Kg <= (128/GS) * nthr since nthr >= K/16
     constexpr int SPT = GS >= 128 ? 1 : 128 / GS;
     extern __shared__ __align__(16) unsigned char smem[];
+    __shared__ float s_norm_inv;
 
     const int K = a.K;
     const int Kg = K / GS;
@@ -129,11 +130,16 @@ __global__ __launch_bounds__(GEMV_MAX_THREADS) void gemv_kernel(GemvArgs a, int 
     // ld words per chain: [r*8 + lane][g] (lanes) or [m*R + r][g] (general).
     const int ld = group_ld(Kg);
     const int acc_words = (LANES ? 8 * R : MR * R) * ld;
-    // >= K (activation staging, 4 float4 per thread: 16*nthr words) and
-    // >= 2*nthr (argmax scratch)
-    int stage_words = acc_words > 16 * nthr ? acc_words : 16 * nthr;
+    // >= K (activation staging, 4 float4 per thread: 16*nthr words), plus
+    // the chain-major copy of the row for a fused norm (8 rows of K/8 + 4),
+    // and >= 2*nthr (argmax scratch)
+    const bool has_norm = a.norm_w != nullptr;
+    const int nrs = K / 8 + 4;
+    const int stage_need = 16 * nthr + (has_norm ? 8 * nrs : 0);
+    int stage_words = acc_words > stage_need ? acc_words : stage_need;
     int32_t *accb = reinterpret_cast<int32_t *>(smem);
     float *xs = reinterpret_cast<float *>(smem);  // phase 0 only (aliases accb)
+    float *xn = xs + 16 * nthr;                   // [8][nrs]: x[l + 8j] at l*nrs + j
     float *as_l = reinterpret_cast<float *>(smem) + stage_words;  // [M][Kg]
     float *sc_l = as_l + MR * Kg;                                   // [R][ld]
     float *ybuf = sc_l + R * ld;                                    // [MR][R]
@@ -182,6 +188,13 @@ __global__ __launch_bounds__(GEMV_MAX_THREADS) void gemv_kernel(GemvArgs a, int 
         const float4 x1 = src[i1 < K / 4 ? i1 : 0];
         const float4 x2 = src[i2 < K / 4 ? i2 : 0];
         const float4 x3 = src[i3 < K / 4 ? i3 : 0];
+        // fused norm: this thread's 16 weight bytes and group scale
+        u32x4 nw = (u32x4){0u, 0u, 0u, 0u};
+        float nsc = 0.0f;
+        if (has_norm) {
+            nw = *reinterpret_cast<const u32x4 *>(a.norm_w + 16 * (act ? tid : 0));
+            nsc = a.norm_s[act ? (16 * tid) / GS : 0];
+        }
         if (m == 0) prefetch(resolve(tile));  // grid <= ntiles: every block has a tile
         // keep the loads above ahead of the LDS stores below (the stores wait
         // only for the activation loads, issued first); slots past K/4 exist
@@ -192,7 +205,71 @@ __global__ __launch_bounds__(GEMV_MAX_THREADS) void gemv_kernel(GemvArgs a, int 
         xs4[i1] = x1;
         xs4[i2] = x2;
         xs4[i3] = x3;
+        if (has_norm) {
+            // chain-major copy: element 4i + c sits in chain 4*(i&1) + c at i/2
+            auto put4 = [&](int i, const float4 &v) {
+                if (i < K / 4) {
+                    float *d = xn + 4 * (i & 1) * nrs + (i >> 1);
+                    d[0] = v.x;
+                    d[nrs] = v.y;
+                    d[2 * nrs] = v.z;
+                    d[3 * nrs] = v.w;
+                }
+            };
+            put4(i0, x0);
+            put4(i1, x1);
+            put4(i2, x2);
+            put4(i3, x3);
+        }
         lds_barrier();
+        if (has_norm) {
+            // sum of squares in the reference's 8-lane order (lanes 0..7 of
+            // wave 0), then inv = 1/sqrt(ss/K + eps) in fp32
+            if (tid < 64) {
+                float acc = 0.0f;
+                if (tid < 8) {
+                    const float *row = xn + tid * nrs;
+                    const int cnt = K / 8;
+                    int j = 0;
+                    for (; j + 32 <= cnt; j += 32) {
+                        float4 v[8];
+#pragma unroll
+                        for (int u = 0; u < 8; ++u) v[u] = reinterpret_cast<const float4 *>(row + j)[u];
+#pragma unroll
+                        for (int u = 0; u < 8; ++u) {
+                            acc = fmaf(v[u].x, v[u].x, acc);
+                            acc = fmaf(v[u].y, v[u].y, acc);
+                            acc = fmaf(v[u].z, v[u].z, acc);
+                            acc = fmaf(v[u].w, v[u].w, acc);
+                        }
+                    }
+                    for (; j < cnt; ++j) acc = fmaf(row[j], row[j], acc);
+                }
+                float ss = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, acc), 0));
+#pragma unroll
+                for (int l = 1; l < 8; ++l)
+                    ss = ss + __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, acc), l));
+                if (tid == 0) s_norm_inv = rcp_rn(sqrt_rn(ss * rcp_rn((float)K) + a.norm_eps));
+            }
+            lds_barrier();
+            if (act) {
+                // this thread's 16 elements: x = w * ((s_g * inv) * x)
+                const float comb = nsc * s_norm_inv;
+                const uint32_t wd[4] = {nw.x, nw.y, nw.z, nw.w};
+                float4 *xc4 = reinterpret_cast<float4 *>(xs + 16 * tid);
+#pragma unroll
+                for (int q4 = 0; q4 < 4; ++q4) {
+                    float4 v = xc4[q4];
+                    const uint32_t w = wd[q4];
+                    v.x = (float)(int8_t)(w & 0xFF) * (comb * v.x);
+                    v.y = (float)(int8_t)((w >> 8) & 0xFF) * (comb * v.y);
+                    v.z = (float)(int8_t)((w >> 16) & 0xFF) * (comb * v.z);
+                    v.w = (float)(int8_t)(w >> 24) * (comb * v.w);
+                    xc4[q4] = v;
+                }
+            }
+            lds_barrier();
+        }
         if (act) {
             // Every thread of a group recomputes the group's sum of squares
             // from LDS in the reference order: 16 FMA chains over the gs/16
@@ -508,7 +585,8 @@ static hipError_t launch_gemv_t(const GemvArgs &a, int *grid_out, hipStream_t st
     const int nthr = K / 16 > 64 ? K / 16 : 64;
     const int ld = group_ld(Kg);
     const int acc_words = (LANES ? 8 * R : MR * R) * ld;
-    const int stage_words = acc_words > 16 * nthr ? acc_words : 16 * nthr;
+    const int stage_need = 16 * nthr + (a.norm_w ? 8 * (K / 8 + 4) : 0);
+    const int stage_words = acc_words > stage_need ? acc_words : stage_need;
     const size_t lds = (size_t)(stage_words + MR * Kg + R * ld + MR * R) * 4;
 
     int ntiles = 0;
@@ -546,6 +624,7 @@ static hipError_t launch_gemv_gs(const GemvArgs &a, bool lanes, int *grid_out, h
 hipError_t launch_gemv(const GemvArgs &a, bool lanes, int *grid_out, hipStream_t st) {
     if (a.M < 1 || a.M > 8 || a.K % 16 != 0 || a.K / 16 > GEMV_MAX_THREADS)
         return hipErrorInvalidValue;
+    if (a.norm_w && (a.M != 1 || !a.norm_s)) return hipErrorInvalidValue;
     switch (a.gs) {
         case 16: return launch_gemv_gs<16>(a, lanes, grid_out, st);
         case 32: return launch_gemv_gs<32>(a, lanes, grid_out, st);

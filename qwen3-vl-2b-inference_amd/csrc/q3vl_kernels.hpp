@@ -40,6 +40,13 @@ struct GemvArgs {
     int accumulate;   // GEMV_PLAIN: Y += A W^T (the decode step's residual add)
     float *part_val;  // GEMV_ARGMAX: [grid, M] block partial maxima
     int32_t *part_idx;  // [grid, M] block partial indices (-1: none)
+    // Optional RMSNorm of the activation row before quantization (M == 1):
+    // A' = w * ((s_g * inv) * A), inv = 1/sqrt(sum(A^2)/K + eps) with the sum
+    // in the 8-lane order (text_layer.cpp:110-147 / 234-270, int8 group
+    // weight with the GEMV's group size). norm_w == nullptr: no norm.
+    const int8_t *norm_w;
+    const float *norm_s;
+    float norm_eps;
 };
 
 // lanes=true: the reference's M=1 path (i8:122-224 / 327-455) -- per-lane
@@ -78,10 +85,6 @@ struct AttnArgs {
 };
 hipError_t launch_embed(const int8_t *w, const float *s, const int32_t *token, float *x, int H,
                         int gs, hipStream_t st);
-// rms_norm / rms_norm_inplace with an int8 group weight (same result), one
-// row of n <= 8192, n % 8 == 0.
-hipError_t launch_rmsnorm_i8(const float *x, const int8_t *w, const float *ws, float *out, int n,
-                             int gs, float eps, hipStream_t st);
 hipError_t launch_attention(const AttnArgs &a, hipStream_t st);
 constexpr int kAttnChunk = 64;  // positions per attention score chunk
 // LDS the softmax/value kernel needs; at most kAttnMaxLds.
