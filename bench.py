@@ -377,6 +377,47 @@ def cpu_baseline_cfg0(budget_s):
                 kind="reference", sample=f"{len(times)} calls of linear() M=1 N=6144 K=2048, median {med * 1e3:.3f} ms")
 
 
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_gemv_traffic.json")
+
+
+def pmc_workload():
+    """Workload for the HBM-traffic counter passes (rocprofv3 --pmc
+    FETCH_SIZE, then WRITE_SIZE): an elementwise dst = src + 1 over 256 MiB of
+    uint8 (the calibration kernel: 256 MiB read, 256 MiB written) and then 3
+    eager decode steps of config 1, whose gemv_kernel dispatches are the
+    measured kernel."""
+    import torch
+    from q3vl_int8 import model as qm
+    n = 256 << 20
+    src = torch.ones(n, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    torch.add(src, 1, out=dst)
+    torch.cuda.synchronize()
+    dims = decode_dims(max_seq=CTX + 16)
+    m, k16, v16 = build_model(dims, 0xD0C0DE)
+    model = qm.DeviceTextModel(dims, m)
+    kd = torch.from_numpy(k16.view("int16")).cuda()
+    vd = torch.from_numpy(v16.view("int16")).cuda()
+    tok = torch.tensor([5], dtype=torch.int32, device="cuda")
+    pos = torch.tensor([CTX], dtype=torch.int32, device="cuda")
+    ws = qm.alloc_decode_workspace(model)
+    for _ in range(3):
+        qm.decode_step(model, kd, vd, tok, pos, None, ws)
+    torch.cuda.synchronize()
+    log("pmc workload done")
+
+
+def load_traffic():
+    """HBM bytes per gemv_kernel launch from the committed counter summary
+    (FETCH_SIZE + WRITE_SIZE per dispatch, scaled by the copy calibration)."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            return json.load(f)
+    except (OSError, ValueError):
+        return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -385,6 +426,8 @@ def main():
     ap.add_argument("--configs", default="cfg1,cfg0,cfg2,cfg3,cfg4")
     ap.add_argument("--cpu-budget", type=float, default=15.0,
                     help="seconds of reference CPU decode for cpu_baseline (0: skip)")
+    ap.add_argument("--pmc-workload", action="store_true",
+                    help="run only the workload of the HBM-traffic counter passes")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (see the sharding "
@@ -394,6 +437,9 @@ def main():
     import q3vl_int8 as q
     q.lib()  # fails loudly if the HIP library is missing
     torch.cuda.set_device(0)
+    if args.pmc_workload:
+        pmc_workload()
+        return
     configs = args.configs.split(",")
     dims = decode_dims(max_seq=(CTX + args.warmup + args.steps + 7 + 15) // 8 * 8)
     results, cpu, m = [], None, None
@@ -423,6 +469,7 @@ def main():
         if "cfg0_up_proj_gemv" in by:
             by["cfg0_up_proj_gemv"]["cpu_reference"] = cpu_baseline_cfg0(min(5.0, args.cpu_budget))
     rf = head["gemv_roofline"]
+    tr = load_traffic()
     line = {
         "metric": "decode tok/s, Qwen3-VL-2B text decoder (int8 group-64 weights), 1 GPU",
         "value": round(head["value"], 2),
@@ -442,7 +489,8 @@ def main():
                                "batch 1, HIP graph per step",
                    "global_batch": 1, "context": CTX},
         "roofline": {"bound": "hbm", "achieved": round(rf["achieved_GBs"], 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(rf["frac"], 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(rf["frac"], 4),
+                     "traffic": round(tr["hbm_bytes_per_launch"]) if tr else None,
                      "kernel": rf["kernel"], "bytes_per_launch": round(rf["bytes_per_launch"]),
                      "avg_launch_us": round(rf["avg_launch_us"], 3)},
         "cpu_baseline": cpu,

@@ -19,6 +19,8 @@
 // In SwiGLU mode the block's 128 B rows are 64 gate rows and the same 64 up
 // rows, and each wave holds a gate tile and the matching up tile so the
 // epilogue silu(g)*u needs no exchange.
+#include <stdlib.h>
+
 #include "q3vl_device.hpp"
 #include "q3vl_kernels.hpp"
 
@@ -288,11 +290,245 @@ __global__ __launch_bounds__(256, 2) void gemm_i8_kernel(GemmArgs a) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// gemm_g64_kernel: the same numerics for group size 64 (the model's), built
+// so the matrix cores and the fp32 epilogue overlap.
+//
+// * One K-step = one group (BK = gs = 64). The group's epilogue is
+//   out = fma(float(G)*a_s, w_s, out) in reference order. Two blocks share
+//   each CU (240 VGPRs at 128x128), so one wave's VALU epilogue overlaps the
+//   other's MFMAs. The first MFMA of a group takes C = 0 (no clearing).
+//   (Measured alternatives that did not pay: a second accumulator set per
+//   wave to overlap within the wave -- it spills at 128x128 -- and global
+//   loads more than one K-step ahead.)
+// * B is widened to fp16 once per block when the stage is written to LDS
+//   (not once per wave); A arrives as exact fp16 images of the int16
+//   activations. Both stages are [rows][64] fp16 with XOR-swizzled 16-byte
+//   slots.
+// * Scales live in a ring of three LDS slots indexed by group.
+// * Tile (32*MT*2) x (32*NT*2), 4 waves in 2x2, each wave (32*MT) x (32*NT);
+//   the host picks MT/NT so the grid fills the device. SWIGLU (NT = 2): the
+//   block's B rows 0..63 are gate rows, 64..127 the same up rows.
+template <int MT, int NT, bool SWIGLU>
+__global__ __launch_bounds__(256, 2) void gemm_g64_kernel(GemmArgs a) {
+    constexpr int TBM = 64 * MT, TBN = 64 * NT;
+    constexpr int ASTG = TBM * 128, BSTG = TBN * 128;  // bytes per stage (fp16)
+    constexpr int SCW = TBM + TBN;                      // floats per scale slot
+    constexpr int ACH = TBM * 8 / 256;                  // A 16-byte chunks per thread
+    constexpr int BCH = TBN * 4 / 256;                  // B 16-byte int8 chunks per thread
+    extern __shared__ __align__(16) unsigned char smem[];
+    auto As = [&](int b) { return smem + b * ASTG; };
+    auto Bs = [&](int b) { return smem + 2 * ASTG + b * BSTG; };
+    float *scr = reinterpret_cast<float *>(smem + 2 * (ASTG + BSTG));  // [3][SCW]
+
+    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    const int wm = wid & 1, wn = wid >> 1;
+    const int l32 = lane & 31, h = lane >> 5;
+    const int M = a.M, N = a.N, K = a.K;
+    const int Kg = K / 64;
+    const int m0 = blockIdx.y * TBM;
+    const int ncols = SWIGLU ? TBN / 2 : TBN;
+    const int n0 = blockIdx.x * ncols;
+
+    // ---- staging assignment (element offsets at k = 0)
+    uint32_t a_off[ACH];
+    int a_dst[ACH];
+#pragma unroll
+    for (int i = 0; i < ACH; ++i) {
+        const int c = tid + 256 * i;
+        const int row = c >> 3, slot = c & 7;
+        a_off[i] = (uint32_t)min(m0 + row, M - 1) * (uint32_t)a.lda + slot * 8;
+        a_dst[i] = row * 128 + ((slot ^ ((row >> 1) & 7)) << 4);
+    }
+    uint32_t b_off[BCH];
+    int b_dst0[BCH], b_dst1[BCH];
+    bool b_up[BCH];
+#pragma unroll
+    for (int i = 0; i < BCH; ++i) {
+        const int c = tid + 256 * i;
+        const int row = c >> 2, q = c & 3;  // q-th 16 bytes of the row's 64 int8
+        const bool up = SWIGLU && row >= 64;
+        b_up[i] = up;
+        b_off[i] = (uint32_t)min(n0 + (SWIGLU ? (row & 63) : row), N - 1) * (uint32_t)K + q * 16;
+        const int s0 = 2 * q, s1 = 2 * q + 1, sw = (row >> 1) & 7;
+        b_dst0[i] = row * 128 + ((s0 ^ sw) << 4);
+        b_dst1[i] = row * 128 + ((s1 ^ sw) << 4);
+    }
+    // scale loaders: thread t < TBM loads a_s of row t, TBM <= t < SCW loads
+    // w_s of column t - TBM
+    const bool sc_a = tid < TBM, sc_b = tid >= TBM && tid < SCW;
+    int sc_src = 0;
+    const float *sc_w = nullptr;
+    if (sc_a) sc_src = min(m0 + tid, M - 1);
+    if (sc_b) {
+        const int c = tid - TBM;
+        const bool up = SWIGLU && c >= 64;
+        sc_w = up ? a.S1 : a.S0;
+        sc_src = min(n0 + (SWIGLU ? (c & 63) : c), N - 1) * Kg;
+    }
+
+    // Global loads of K-step kb+1 are in flight during step kb.
+    u32x4 ra[ACH], rb[BCH];
+    float rs = 0.0f;
+    auto load_regs = [&](int kb) {
+        const int k0 = kb * 64;
+#pragma unroll
+        for (int i = 0; i < ACH; ++i) ra[i] = *reinterpret_cast<const u32x4 *>(a.Aq + a_off[i] + k0);
+#pragma unroll
+        for (int i = 0; i < BCH; ++i) {
+            const int8_t *W = b_up[i] ? a.W1 : a.W0;
+            rb[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(W + b_off[i] + k0));
+        }
+        if (sc_a) rs = a.a_s[(size_t)kb * a.lda_s + sc_src];
+        if (sc_b) rs = sc_w[sc_src + kb];
+    };
+    auto store_lds = [&](int buf, int kb) {
+#pragma unroll
+        for (int i = 0; i < ACH; ++i) *reinterpret_cast<u32x4 *>(As(buf) + a_dst[i]) = ra[i];
+#pragma unroll
+        for (int i = 0; i < BCH; ++i) {
+            u32x4 v = rb[i] ^ (u32x4){0x80808080u, 0x80808080u, 0x80808080u, 0x80808080u};
+            uint32_t w[8];
+            widen4(v.x, w[0], w[1]);
+            widen4(v.y, w[2], w[3]);
+            widen4(v.z, w[4], w[5]);
+            widen4(v.w, w[6], w[7]);
+            *reinterpret_cast<u32x4 *>(Bs(buf) + b_dst0[i]) = (u32x4){w[0], w[1], w[2], w[3]};
+            *reinterpret_cast<u32x4 *>(Bs(buf) + b_dst1[i]) = (u32x4){w[4], w[5], w[6], w[7]};
+        }
+        if (tid < SCW) scr[(kb % 3) * SCW + tid] = rs;
+    };
+
+    float16_t acc[MT][NT], out[MT][NT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) out[mt][nt] = (float16_t)(0.0f);
+
+    int arow[MT], brow[NT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) arow[mt] = wm * 32 * MT + mt * 32 + l32;
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+        brow[nt] = SWIGLU ? (nt * 64 + wn * 32 + l32) : (wn * 32 * NT + nt * 32 + l32);
+
+    // MFMAs of one K-step (LDS buffer buf) into C
+    auto mfma_step = [&](int buf, float16_t (&C)[MT][NT]) {
+#pragma unroll
+        for (int hs = 0; hs < 2; ++hs) {
+            half8_t af[MT][2], bf[NT][2];
+            const int s0 = 4 * hs + 2 * h;  // this lane half's 16 k: slots s0, s0+1
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                const int r = arow[mt], sw = (r >> 1) & 7;
+                af[mt][0] = *reinterpret_cast<const half8_t *>(As(buf) + r * 128 + ((s0 ^ sw) << 4));
+                af[mt][1] = *reinterpret_cast<const half8_t *>(As(buf) + r * 128 + (((s0 + 1) ^ sw) << 4));
+            }
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                const int r = brow[nt], sw = (r >> 1) & 7;
+                bf[nt][0] = *reinterpret_cast<const half8_t *>(Bs(buf) + r * 128 + ((s0 ^ sw) << 4));
+                bf[nt][1] = *reinterpret_cast<const half8_t *>(Bs(buf) + r * 128 + (((s0 + 1) ^ sw) << 4));
+            }
+#pragma unroll
+            for (int u = 0; u < 2; ++u)
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                    for (int nt = 0; nt < NT; ++nt)
+                        C[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                            af[mt][u], bf[nt][u], (hs == 0 && u == 0) ? (float16_t)(0.0f) : C[mt][nt],
+                            0, 0, 0);
+        }
+    };
+    // fp32 epilogue of group g from C (reference order)
+    auto epilogue = [&](int g, const float16_t (&C)[MT][NT]) {
+        const float *asT = scr + (g % 3) * SCW;
+        const float *wsT = asT + TBM;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            float asv[16];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const float4 v = *reinterpret_cast<const float4 *>(asT + wm * 32 * MT + mt * 32 + 8 * q + 4 * h);
+                asv[4 * q + 0] = v.x;
+                asv[4 * q + 1] = v.y;
+                asv[4 * q + 2] = v.z;
+                asv[4 * q + 3] = v.w;
+            }
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                const float wsv = wsT[brow[nt]];
+#pragma unroll
+                for (int e = 0; e < 16; ++e) out[mt][nt][e] = fmaf(C[mt][nt][e] * asv[e], wsv, out[mt][nt][e]);
+            }
+        }
+    };
+
+    const int nkb = K / 64;
+    load_regs(0);
+    store_lds(0, 0);
+    __syncthreads();
+    for (int kb = 0; kb < nkb; ++kb) {
+        const int buf = kb & 1;
+        if (kb + 1 < nkb) load_regs(kb + 1);
+        mfma_step(buf, acc);
+        epilogue(kb, acc);
+        if (kb + 1 < nkb) store_lds(buf ^ 1, kb + 1);
+        __syncthreads();
+    }
+
+    // ---- store
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const int mrow = m0 + wm * 32 * MT + mt * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
+            if (mrow >= M) continue;
+            if constexpr (SWIGLU) {
+                const int ncol = n0 + wn * 32 + l32;
+                if (ncol < N) a.C[(size_t)mrow * N + ncol] = silu_mul(out[mt][0][e], out[mt][1][e]);
+            } else {
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) {
+                    const int ncol = n0 + brow[nt];
+                    if (ncol < N) a.C[(size_t)mrow * N + ncol] = out[mt][nt][e];
+                }
+            }
+        }
+    }
+}
+
+template <int MT, int NT, bool SWIGLU>
+static hipError_t launch_g64(const GemmArgs &a, hipStream_t st) {
+    constexpr int TBM = 64 * MT, TBN = 64 * NT;
+    const int ncols = SWIGLU ? TBN / 2 : TBN;
+    dim3 grid((a.N + ncols - 1) / ncols, (a.M + TBM - 1) / TBM);
+    const size_t lds = 2 * (TBM + TBN) * 128 + 3 * (TBM + TBN) * 4;
+    static bool attr_set = false;  // raise the dynamic LDS limit once
+    if (!attr_set) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemm_g64_kernel<MT, NT, SWIGLU>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+        attr_set = true;
+    }
+    gemm_g64_kernel<MT, NT, SWIGLU><<<grid, 256, lds, st>>>(a);
+    return hipGetLastError();
+}
+
 hipError_t launch_gemm(const GemmArgs &a, hipStream_t st) {
     // gs <= 128 keeps every in-group fp32 partial sum below 2^24 (exact).
     if (a.K % BK != 0 || (a.gs != 32 && a.gs != 64 && a.gs != 128))
         return hipErrorInvalidValue;
     if (a.swiglu && a.G) return hipErrorInvalidValue;
+    if (a.gs == 64 && !a.G) {
+        // tile choice: the largest whose grid covers the device's CUs
+        if (a.swiglu) return launch_g64<2, 2, true>(a, st);
+        auto tiles = [&](int bm, int bn) { return ((a.M + bm - 1) / bm) * ((a.N + bn - 1) / bn); };
+        if (tiles(128, 128) >= 256) return launch_g64<2, 2, false>(a, st);
+        if (tiles(64, 128) >= 256) return launch_g64<1, 2, false>(a, st);
+        return launch_g64<1, 1, false>(a, st);
+    }
     const int nb = a.swiglu ? BN / 2 : BN;
     dim3 grid((a.N + nb - 1) / nb, (a.M + BM - 1) / BM);
     const size_t lds = 2 * (A_STAGE + B_STAGE + SC_STAGE);

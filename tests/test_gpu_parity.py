@@ -89,7 +89,10 @@ def run_linear_case(orc, M, N, K, gs, seed, groups):
     dA, dW, dS = dev(A), dev(W), dev(S)
     G = torch.zeros((M, N, K // gs), dtype=torch.int32, device="cuda") if groups else None
     C = q.linear_i8(dA, dW, dS, gs, groups=G)
-    C_ref, G_ref = orc.linear(A, W, S, gs, groups=True)
+    if groups:
+        C_ref, G_ref = orc.linear(A, W, S, gs, groups=True)
+    else:
+        C_ref = orc.linear(A, W, S, gs)
     assert_bits_equal(host(C), C_ref, f"C {M}x{N}x{K} gs{gs}")
     if groups:
         np.testing.assert_array_equal(host(G), G_ref)
@@ -110,6 +113,24 @@ def test_general_gemv_parity(orc, M, N, K, gs):
 @pytest.mark.parametrize("M,N,K,gs", GEMM, ids=[str(c) for c in GEMM])
 def test_gemm_parity(orc, M, N, K, gs):
     run_linear_case(orc, M, N, K, gs, seed=M + N + K, groups=M * N * K <= 64 * 512 * 2048)
+
+
+@pytest.mark.parametrize("M,N,K", [(9, 128, 1024), (100, 200, 2048), (130, 260, 1024),
+                                   (784, 3072, 1024), (196, 2048, 4096), (512, 8192, 1024),
+                                   (513, 8200, 1024)])
+def test_gemm_group64_tiles_parity(orc, M, N, K):
+    """The group-64 MFMA GEMM at each of its tile shapes (64x64, 64x128,
+    128x128 chosen by grid size), ragged M and N, bit-exact."""
+    run_linear_case(orc, M, N, K, 64, seed=7 * M + N + K, groups=False)
+
+
+@pytest.mark.parametrize("M,N,K", [(100, 200, 1024), (333, 1030, 2048)])
+def test_gemm_swiglu_ragged_parity(orc, M, N, K):
+    A, Wg, Sg = make_case(900 + M, M, N, K, 64)
+    _, Wu, Su = make_case(901 + M, M, N, K, 64)
+    H = host(q.linear_i8_swiglu(dev(A), dev(Wg), dev(Sg), dev(Wu), dev(Su), 64))
+    H_ref = orc.swiglu(orc.linear(A, Wg, Sg, 64), orc.linear(A, Wu, Su, 64))
+    np.testing.assert_array_equal(H.view(np.uint32), H_ref.view(np.uint32))
 
 
 def test_golden_vectors_on_gpu():
