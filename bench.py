@@ -176,7 +176,8 @@ def decode_gemv_roofline(model, dims):
     weights (the lm_head in plain mode). Each class of launch (qkv, o,
     gate/up, down over the 28 layers; lm_head four times) is captured in a
     HIP graph and replayed between HIP events on the capturing stream, so
-    launch gaps vanish and time / launches is the average kernel duration.
+    launch gaps vanish and time / launches is the average kernel duration
+    (median of five timed trials).
     achieved = one step's algorithmic bytes / one step's summed durations."""
     import torch
     import q3vl_int8 as q
@@ -217,20 +218,22 @@ def decode_gemv_roofline(model, dims):
         g.replay()
         torch.cuda.synchronize()
         st = torch.cuda.current_stream()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        reps = 5
-        e0.record(st)
-        for _ in range(reps):
-            g.replay()
-        e1.record(st)
-        torch.cuda.synchronize()
-        us = e0.elapsed_time(e1) * 1e3 / (reps * len(fns))
+        reps, trials = 5, []
+        for _ in range(5):  # median of 5 timed trials of 5 replays each
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(st)
+            for _ in range(reps):
+                g.replay()
+            e1.record(st)
+            torch.cuda.synchronize()
+            trials.append(e0.elapsed_time(e1) * 1e3 / (reps * len(fns)))
+        us = sorted(trials)[len(trials) // 2]
         res[name] = dict(us=us, bytes=nbytes, GBs=nbytes / (us * 1e-6) / 1e9)
     step_us = sum(res[k]["us"] * n for k, n in per_step.items())
     step_bytes = sum(res[k]["bytes"] * n for k, n in per_step.items())
     launches = sum(per_step.values())
     gbs = step_bytes / (step_us * 1e-6) / 1e9
-    return dict(kernel="gemv_kernel<64, 1, true>", launches=launches,
+    return dict(kernel="gemv_kernel<64, 1, true, R> (R = rows per tile: 2, 4 or 8 by shape)", launches=launches,
                 bytes_per_launch=step_bytes / launches, avg_launch_us=step_us / launches,
                 achieved_GBs=gbs, frac=gbs / HBM_PEAK_GBS, step_gemv_us=step_us, by_class=res)
 

@@ -28,7 +28,7 @@ namespace q3vl {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int GEMV_R = 8;          // weight rows per tile
+constexpr int GEMV_R = 8;          // weight rows per tile (general path; the lane path picks 2, 4 or 8)
 constexpr int GEMV_MAX_THREADS = 512;  // => K <= 8192 on this path
 constexpr int GEMV_MAX_GRID = 8192;    // the C ABI reserves this many argmax partials
 
@@ -74,13 +74,12 @@ struct Tile {
     int tseg, tn0, tN;
 };
 
-template <int GS, int MR, bool LANES>
+template <int GS, int MR, bool LANES, int R>
 __global__ __launch_bounds__(GEMV_MAX_THREADS) void gemv_kernel(GemvArgs a, int ntiles) {
     constexpr int T = GS / 16;
-    constexpr int R = GEMV_R;
     constexpr int HALF = R / 2;
-    // scale values per thread per tile: R*Kg <= (128/GS) * nthr since nthr >= K/16
-    constexpr int SPT = GS >= 128 ? 1 : 128 / GS;
+    // scale values per thread per tile: R*Kg <= (16R/GS) * nthr since nthr >= K/16
+    constexpr int SPT = 16 * R >= GS ? 16 * R / GS : 1;
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ float s_norm_inv;
 
@@ -578,9 +577,8 @@ __global__ void swiglu_kernel(float *gate, const float *up, size_t n) {
 }
 
 // ------------------------------------------------------------------ launch
-template <int GS, int MR, bool LANES>
+template <int GS, int MR, bool LANES, int R>
 static hipError_t launch_gemv_t(const GemvArgs &a, int *grid_out, hipStream_t st) {
-    constexpr int R = GEMV_R;
     const int K = a.K, Kg = K / GS;
     const int nthr = K / 16 > 64 ? K / 16 : 64;
     const int ld = group_ld(Kg);
@@ -600,7 +598,7 @@ static hipError_t launch_gemv_t(const GemvArgs &a, int *grid_out, hipStream_t st
     if (e != hipSuccess) return e;
     e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
     if (e != hipSuccess) return e;
-    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, gemv_kernel<GS, MR, LANES>, nthr, lds);
+    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, gemv_kernel<GS, MR, LANES, R>, nthr, lds);
     if (e != hipSuccess) return e;
     if (occ < 1) occ = 1;
     int grid = cus * occ;
@@ -608,17 +606,41 @@ static hipError_t launch_gemv_t(const GemvArgs &a, int *grid_out, hipStream_t st
     if (grid > ntiles) grid = ntiles;
     if (grid < 1) grid = 1;
     if (grid_out) *grid_out = grid;
-    gemv_kernel<GS, MR, LANES><<<grid, nthr, lds, st>>>(a, ntiles);
+    gemv_kernel<GS, MR, LANES, R><<<grid, nthr, lds, st>>>(a, ntiles);
     return hipGetLastError();
+}
+
+// Rows per tile of the M = 1 lane path: the largest of 8, 4, 2 that still
+// gives about four tiles per CU. Small GEMVs (one tile per block) are bound by
+// the latency of each block's dependent phases, so more and smaller blocks
+// let those phases overlap across waves; each block repeats the activation
+// quantization, which grows with K, so long rows (K > 4096) keep 8 rows.
+static int lane_rows(const GemvArgs &a) {
+    if (a.K > 4096) return 8;
+    auto tiles = [&](int r) {
+        if (a.mode == GEMV_SWIGLU) return (a.seg[0].N + r / 2 - 1) / (r / 2);
+        int t = 0;
+        for (int s = 0; s < a.nseg; ++s) t += (a.seg[s].N + r - 1) / r;
+        return t;
+    };
+    if (tiles(8) >= 1024) return 8;
+    if (tiles(4) >= 1024) return 4;
+    return 2;
 }
 
 template <int GS>
 static hipError_t launch_gemv_gs(const GemvArgs &a, bool lanes, int *grid_out, hipStream_t st) {
-    if (lanes) return launch_gemv_t<GS, 1, true>(a, grid_out, st);
-    if (a.M <= 1) return launch_gemv_t<GS, 1, false>(a, grid_out, st);
-    if (a.M <= 2) return launch_gemv_t<GS, 2, false>(a, grid_out, st);
-    if (a.M <= 4) return launch_gemv_t<GS, 4, false>(a, grid_out, st);
-    return launch_gemv_t<GS, 8, false>(a, grid_out, st);
+    if (lanes) {
+        switch (lane_rows(a)) {
+            case 2: return launch_gemv_t<GS, 1, true, 2>(a, grid_out, st);
+            case 4: return launch_gemv_t<GS, 1, true, 4>(a, grid_out, st);
+            default: return launch_gemv_t<GS, 1, true, 8>(a, grid_out, st);
+        }
+    }
+    if (a.M <= 1) return launch_gemv_t<GS, 1, false, GEMV_R>(a, grid_out, st);
+    if (a.M <= 2) return launch_gemv_t<GS, 2, false, GEMV_R>(a, grid_out, st);
+    if (a.M <= 4) return launch_gemv_t<GS, 4, false, GEMV_R>(a, grid_out, st);
+    return launch_gemv_t<GS, 8, false, GEMV_R>(a, grid_out, st);
 }
 
 hipError_t launch_gemv(const GemvArgs &a, bool lanes, int *grid_out, hipStream_t st) {
