@@ -486,7 +486,7 @@ int q3vl_decode_step(const q3vl_text_model *m, uint16_t *k_cache, uint16_t *v_ca
     float *pv = reinterpret_cast<float *>(w + L.lin + LL.parts_val);
     int32_t *pi = reinterpret_cast<int32_t *>(w + L.lin + LL.parts_idx);
 
-    Q3VL_HIP(launch_embed(m->embed_w, m->embed_s, token, x, H, gs, st), "embed");  // :478-485
+    Q3VL_HIP(launch_embed(m->embed_w, m->embed_s, token, x, H, gs, V, st), "embed");  // :478-485
     AttnArgs aa{};
     aa.q = q;
     aa.k = k;

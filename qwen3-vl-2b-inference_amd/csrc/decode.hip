@@ -66,6 +66,37 @@ __device__ __forceinline__ uint16_t f2h(float f) {
     return (uint16_t)(sign | r);
 }
 
+// s_waitcnt lgkmcnt(0) alone. A batch of 16 LDS reads issued behind another
+// 16 exceeds what the 4-bit lgkm counter can tell apart, so the compiler's
+// own wait before the first batch's use would also wait for most of the
+// second; waiting for the first batch before issuing the second avoids that.
+__device__ __forceinline__ void lgkm_wait0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
+
+// Four chain steps acc = fma(p_c of lane k of this row of 16 lanes, v_c, acc),
+// c = 0..3: v_fmac_f32 with the DPP row_newbcast:k operand, one instruction
+// per step (the row broadcast replaces an LDS read of p per step). One asm
+// block holds the four steps, so no wait states are placed between them; the
+// caller keeps 2 instructions between a VALU write of p and its first use.
+#define Q3VL_FMAC4_BC(K)                                                                        \
+    case K:                                                                                     \
+        asm volatile("v_fmac_f32_dpp %0, %1, %5 row_newbcast:" #K " row_mask:0xf bank_mask:0xf\n\t" \
+                     "v_fmac_f32_dpp %0, %2, %6 row_newbcast:" #K " row_mask:0xf bank_mask:0xf\n\t" \
+                     "v_fmac_f32_dpp %0, %3, %7 row_newbcast:" #K " row_mask:0xf bank_mask:0xf\n\t" \
+                     "v_fmac_f32_dpp %0, %4, %8 row_newbcast:" #K " row_mask:0xf bank_mask:0xf"     \
+                     : "+v"(acc)                                                                \
+                     : "v"(p0), "v"(p1), "v"(p2), "v"(p3), "v"(v.x), "v"(v.y), "v"(v.z), "v"(v.w)); \
+        break;
+__device__ __forceinline__ void fmac4_row_bcast(float &acc, float p0, float p1, float p2, float p3,
+                                                const float4 &v, int k) {
+    switch (k) {
+        Q3VL_FMAC4_BC(0) Q3VL_FMAC4_BC(1) Q3VL_FMAC4_BC(2) Q3VL_FMAC4_BC(3)
+        Q3VL_FMAC4_BC(4) Q3VL_FMAC4_BC(5) Q3VL_FMAC4_BC(6) Q3VL_FMAC4_BC(7)
+        Q3VL_FMAC4_BC(8) Q3VL_FMAC4_BC(9) Q3VL_FMAC4_BC(10) Q3VL_FMAC4_BC(11)
+        Q3VL_FMAC4_BC(12) Q3VL_FMAC4_BC(13) Q3VL_FMAC4_BC(14) Q3VL_FMAC4_BC(15)
+    }
+}
+#undef Q3VL_FMAC4_BC
+
 __device__ __forceinline__ float readlane_f(float v, int lane) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
 }
@@ -102,29 +133,63 @@ __device__ __forceinline__ float wave_sumsq128(float lo, float hi) {
 
 // layers/src/text_layer.cpp:240-270 (int8 group weight, in place) on one
 // head of 128 held by a wave, then RoPE (text_layer.cpp:712-760) with the
-// pair (x[i], x[i+64]) in one lane.
-__device__ __forceinline__ void norm_rope128(float &lo, float &hi, const int8_t *w, const float *ws,
-                                             int gs, float eps, float c, float s, int lane) {
-    const float ss = wave_sumsq128(lo, hi);
+// pair (x[i], x[i+64]) in one lane. The lane's inputs are loaded beforehand
+// (NormRopeIn) so that their loads can be issued ahead of larger ones.
+struct NormRopeIn {
+    float lo, hi;  // x[lane], x[lane + 64]
+    int wl, wh;    // int8 norm weights of the two elements (converted at use)
+    float sl, sh;  // their group scales
+    float c, s;    // rope cos / sin at (pos, lane)
+};
+
+__device__ __forceinline__ NormRopeIn load_norm_rope(const float *x, const int8_t *w,
+                                                     const float *ws, int gs,
+                                                     const float *cosr, const float *sinr,
+                                                     int lane) {
+    NormRopeIn r;
+    r.lo = x[lane];
+    r.hi = x[lane + 64];
+    r.wl = w[lane];
+    r.wh = w[lane + 64];
+    r.sl = ws[lane / gs];
+    r.sh = ws[(lane + 64) / gs];
+    r.c = cosr[lane];
+    r.s = sinr[lane];
+    return r;
+}
+
+__device__ __forceinline__ void norm_rope128(const NormRopeIn &in, float eps, float &lo, float &hi) {
+    // opaque copies: keeps the int8 -> float conversions (and their waits)
+    // here rather than next to the loads
+    int wl = in.wl, wh = in.wh;
+    asm volatile("" : "+v"(wl), "+v"(wh));
+    const float ss = wave_sumsq128(in.lo, in.hi);
     const float inv = rcp_rn(sqrt_rn(ss * (1.0f / 128.0f) + eps));  // 1.0f / sqrtf(...)
-    lo = (float)w[lane] * ((ws[lane / gs] * inv) * lo);
-    hi = (float)w[lane + 64] * ((ws[(lane + 64) / gs] * inv) * hi);
-    const float a = lo, b = hi;
-    lo = fmaf(a, c, -(b * s));
-    hi = fmaf(a, s, b * c);
+    const float a = (float)wl * ((in.sl * inv) * in.lo);
+    const float b = (float)wh * ((in.sh * inv) * in.hi);
+    lo = fmaf(a, in.c, -(b * in.s));
+    hi = fmaf(a, in.s, b * in.c);
 }
 
 // ----------------------------------------------------------------- embedding
-// layers/src/text_layer.cpp:3-49, int8 group-quantized table.
+// layers/src/text_layer.cpp:3-49, int8 group-quantized table. A token outside
+// [0, vocab) gives a NaN row instead of a read outside the table.
 __global__ __launch_bounds__(256) void embed_kernel(const int8_t *w, const float *s,
                                                     const int32_t *token, float *x, int H,
-                                                    int gs) {
-    const size_t base = (size_t)(*token) * H;
+                                                    int gs, int vocab) {
+    const int tok = *token;
+    const bool ok = tok >= 0 && tok < vocab;
+    const size_t base = (size_t)(ok ? tok : 0) * H;
     for (int i = threadIdx.x + blockIdx.x * blockDim.x; i < H; i += blockDim.x * gridDim.x)
-        x[i] = (float)w[base + i] * s[(base + i) / gs];
+        x[i] = ok ? (float)w[base + i] * s[(base + i) / gs] : __builtin_nanf("");
 }
 
 // --------------------------------------------------------------- attention
+// Two kernels per layer. Their blocks are numbered kv head first (blockIdx.x
+// = kv head), so with 8 kv heads every block of one kv head sits on the same
+// XCD (workgroups go round-robin over the 8 XCDs) and the scores one kernel
+// writes are read back from that XCD's L2.
+//
 // A: per (kv head, chunk of ATT_CH positions), one wave per query head of the
 // group. The waves normalize + rotate their query heads (q RMSNorm + RoPE,
 // forward.cpp:531-545); the chunk holding `pos` also normalizes + rotates the
@@ -135,64 +200,90 @@ __global__ __launch_bounds__(256) void embed_kernel(const int8_t *w, const float
 constexpr int ATT_CH = 64;
 constexpr int ATT_HD = 128;
 constexpr int ATT_KSTR = ATT_HD + 8;  // halves per LDS key row (272 B: bank-spread)
+constexpr int ATT_THREADS = 256;
+constexpr int ATT_KITEMS = ATT_CH * (ATT_HD / 8) / ATT_THREADS;  // 16-byte key pieces per thread
 
-__global__ __launch_bounds__(256) void attn_scores_kernel(AttnArgs a) {
-    __shared__ float qsh[4][ATT_HD];
+__global__ __launch_bounds__(ATT_THREADS) void attn_scores_kernel(AttnArgs a) {
+    __shared__ float qsh[3][ATT_HD];
     __shared__ uint16_t ksh[ATT_CH * ATT_KSTR];
-    __shared__ uint16_t knew[ATT_HD];
+    __shared__ __align__(16) uint16_t knew[ATT_HD];
     const int kvh = blockIdx.x, ch = blockIdx.y;
     const int pos = *a.pos;
     const int n = pos + 1;
     const int t0 = ch * ATT_CH;
     if (t0 >= n) return;  // uniform: chunk past the context
     const int kvm = a.heads / a.kv_heads;
-    const int wid = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const float c = a.rope_cos[(size_t)pos * (ATT_HD / 2) + lane];
-    const float s = a.rope_sin[(size_t)pos * (ATT_HD / 2) + lane];
-    const size_t lay = (size_t)a.layer * a.kv_heads * a.max_seq * ATT_HD;
-    uint16_t *kc = a.k_cache + lay + (size_t)kvh * a.max_seq * ATT_HD;
-    uint16_t *vc = a.v_cache + lay + (size_t)kvh * a.max_seq * ATT_HD;
+    const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63;
+    const size_t lay = ((size_t)a.layer * a.kv_heads + kvh) * a.max_seq * ATT_HD;
+    uint16_t *kc = a.k_cache + lay;
+    uint16_t *vc = a.v_cache + lay;
     const bool own_pos = pos >= t0 && pos < t0 + ATT_CH;
+    const bool nr_q = wid < kvm, nr_k = wid == kvm && own_pos;
 
-    if (wid < kvm) {
-        const int h = kvh * kvm + wid;
-        float lo = a.q[h * ATT_HD + lane], hi = a.q[h * ATT_HD + 64 + lane];
-        norm_rope128(lo, hi, a.qnorm_w, a.qnorm_s, a.gs, a.eps, c, s, lane);
+    // Issue order: the norm/rope inputs, then the key tile (vmcnt retires in
+    // order, so the norm waits only for its own loads).
+    NormRopeIn nri{};
+    float vlo = 0.0f, vhi = 0.0f;
+    if (nr_q || nr_k) {
+        const float *cosr = a.rope_cos + (size_t)pos * (ATT_HD / 2);
+        const float *sinr = a.rope_sin + (size_t)pos * (ATT_HD / 2);
+        if (nr_q) {
+            nri = load_norm_rope(a.q + (kvh * kvm + wid) * ATT_HD, a.qnorm_w, a.qnorm_s, a.gs,
+                                 cosr, sinr, lane);
+        } else {
+            nri = load_norm_rope(a.k + kvh * ATT_HD, a.knorm_w, a.knorm_s, a.gs, cosr, sinr, lane);
+            vlo = a.v[kvh * ATT_HD + lane];
+            vhi = a.v[kvh * ATT_HD + 64 + lane];
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // key tile rows clamped into the context; row pos is replaced by knew
+    u32x4 kr[ATT_KITEMS];
+#pragma unroll
+    for (int it = 0; it < ATT_KITEMS; ++it) {
+        const int idx = it * ATT_THREADS + tid, r = idx >> 4, c8 = idx & 15;
+        kr[it] = *reinterpret_cast<const u32x4 *>(kc + (size_t)min(t0 + r, n - 1) * ATT_HD + c8 * 8);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    if (nr_q) {
+        float lo, hi;
+        norm_rope128(nri, a.eps, lo, hi);
         qsh[wid][lane] = lo;
         qsh[wid][lane + 64] = hi;
-    } else if (wid == kvm && own_pos) {
-        float lo = a.k[kvh * ATT_HD + lane], hi = a.k[kvh * ATT_HD + 64 + lane];
-        norm_rope128(lo, hi, a.knorm_w, a.knorm_s, a.gs, a.eps, c, s, lane);
+    } else if (nr_k) {
+        float lo, hi;
+        norm_rope128(nri, a.eps, lo, hi);
         const uint16_t l16 = f2h(lo), h16 = f2h(hi);
         kc[(size_t)pos * ATT_HD + lane] = l16;
         kc[(size_t)pos * ATT_HD + 64 + lane] = h16;
         knew[lane] = l16;
         knew[lane + 64] = h16;
-        vc[(size_t)pos * ATT_HD + lane] = f2h(a.v[kvh * ATT_HD + lane]);
-        vc[(size_t)pos * ATT_HD + 64 + lane] = f2h(a.v[kvh * ATT_HD + 64 + lane]);
+        vc[(size_t)pos * ATT_HD + lane] = f2h(vlo);
+        vc[(size_t)pos * ATT_HD + 64 + lane] = f2h(vhi);
     }
-    // key tile of the chunk -> LDS (rows at or past pos come from knew)
-    const int rows = min(ATT_CH, n - t0);
-    for (int i = threadIdx.x; i < ATT_CH * (ATT_HD / 8); i += blockDim.x) {
-        const int r = i / (ATT_HD / 8), c8 = i % (ATT_HD / 8);
-        u32x4 v = (u32x4){0u, 0u, 0u, 0u};
-        if (r < rows && t0 + r != pos)
-            v = *reinterpret_cast<const u32x4 *>(kc + (size_t)(t0 + r) * ATT_HD + c8 * 8);
+    lds_barrier();  // knew
+#pragma unroll
+    for (int it = 0; it < ATT_KITEMS; ++it) {
+        const int idx = it * ATT_THREADS + tid, r = idx >> 4, c8 = idx & 15;
+        const int t = t0 + r;
+        u32x4 v = kr[it];
+        if (t >= n) v = (u32x4){0u, 0u, 0u, 0u};
+        else if (t == pos) v = *reinterpret_cast<const u32x4 *>(knew + c8 * 8);
         *reinterpret_cast<u32x4 *>(ksh + r * ATT_KSTR + c8 * 8) = v;
     }
-    __syncthreads();
-    if (own_pos && threadIdx.x < ATT_HD) ksh[(pos - t0) * ATT_KSTR + threadIdx.x] = knew[threadIdx.x];
-    __syncthreads();
+    lds_barrier();  // ksh, qsh
     if (wid >= kvm) return;
     const int h = kvh * kvm + wid;
     const int t = t0 + lane;
+    const int rows = min(ATT_CH, n - t0);
     float score = -INFINITY;
     if (lane < rows) {
         float cc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-        const uint16_t *kr = ksh + lane * ATT_KSTR;
+        const uint16_t *kr2 = ksh + lane * ATT_KSTR;
 #pragma unroll
         for (int i = 0; i < ATT_HD; i += 8) {
-            const u32x4 kk = *reinterpret_cast<const u32x4 *>(kr + i);
+            const u32x4 kk = *reinterpret_cast<const u32x4 *>(kr2 + i);
             const uint32_t kw[4] = {kk.x, kk.y, kk.z, kk.w};
 #pragma unroll
             for (int l = 0; l < 8; ++l) {
@@ -228,18 +319,19 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(AttnArgs a) {
 //   p_t = e_t * (float)(1/sum)   (all zero if M or sum is not finite/positive),
 //   out[d] = fma chain over t = 0..pos of p_t * v_t[d].
 // The chain is inherently sequential (one dependent FMA per position), so
-// everything else is arranged to keep it to one v_fmac_f32 per step: every
-// global load (the first V chunk, the chunk maxima, up to PV_SREG*PV_THREADS
-// scores per head) is issued at entry; V is widened to fp32 into LDS,
+// everything else is arranged around it. Loads are issued at entry in the
+// order they are needed (chunk maxima, scores, then the first V chunk), so the
+// softmax runs while V is still arriving. V is widened to fp32 into LDS,
 // transposed ([d][t]); p is formed in LDS before the chains start; the chains
-// read 32 positions ahead. e also lives lane-major (row j holds e_j, e_{j+8},
-// ...) so the 8 summing lanes read contiguous 16-byte words.
+// read 32 positions ahead with the reads spread between the FMAs. e also
+// lives lane-major (row j holds e_j, e_{j+8}, ...) so the 8 summing lanes
+// read contiguous 16-byte words.
 constexpr int PV_D = 16;
 constexpr int PV_TC = 1024;
 constexpr int PV_THREADS = 256;
 constexpr int PV_RS = PV_TC + 4;                    // floats per LDS row of vt
-constexpr int PV_ITEMS = PV_TC * (PV_D / 8) / PV_THREADS;  // (position, 8-dim segment) items
-constexpr int PV_SREG = 8;                          // scores held in registers per head
+constexpr int PV_ITEMS = PV_TC * (PV_D / 8) / PV_THREADS;  // 16-byte V pieces per thread
+constexpr int PV_SREG = 4;  // float4 score groups held in registers per head (4096 positions)
 
 // Lane-major e rows hold max_seq/8 terms rounded up to a multiple of 32 (the
 // summing batch), plus 4 floats of padding against bank conflicts.
@@ -251,92 +343,112 @@ __global__ __launch_bounds__(PV_THREADS) void attn_softmax_pv_kernel(AttnArgs a)
     extern __shared__ __align__(16) float smem[];
     const int kvm = a.heads / a.kv_heads;
     const int S = a.max_seq, ets = pv_et_stride(S);
-    float *vt = smem;                       // [PV_D][PV_RS] fp32
-    float *e = smem + PV_D * PV_RS;         // [kvm][S]: e_t, then p_t
+    // e and et first: the chains' p reads then use small constant offsets
+    float *e = smem;                        // [kvm][S]: e_t, then p_t
     float *et = e + kvm * S;                // [kvm][8][ets]
+    float *vt = et + kvm * 8 * ets;         // [PV_D][PV_RS] fp32 (16-byte aligned: S % 8 == 0, ets % 4 == 0)
     __shared__ float hmax[4], hinv[4];
     const int kvh = blockIdx.x, db = blockIdx.y;
     const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63;
     const int n = *a.pos + 1;
     const int nb = n & ~7;
+    const int nch = (n + ATT_CH - 1) / ATT_CH;
     const uint16_t *vc = a.v_cache + ((size_t)a.layer * a.kv_heads + kvh) * S * ATT_HD + db * PV_D;
 
-    // V chunk loads: item -> (8-dim segment sg, position t), one 16-byte
-    // load each, clamped into the context.
+    // ---- entry loads, in order of use. Every load is unconditional (indices
+    // clamped into the buffers), so no wait depends on which were issued.
+    // chunk maxima: wave hh < kvm, lanes c < nch (one pass covers 4096 positions)
+    const int wh = min(wid, kvm - 1);
+    const float cm = a.cmax[(kvh * kvm + wh) * a.max_chunks + min(lane, nch - 1)];
+    // scores: thread tid holds positions 4*(tid + PV_THREADS*k) + 0..3
+    const int kreg = min(PV_SREG, (n + 4 * PV_THREADS - 1) / (4 * PV_THREADS));  // uniform
+    float4 sreg[3][PV_SREG];
+#pragma unroll
+    for (int hh = 0; hh < 3; ++hh) {
+        const float4 *sc = reinterpret_cast<const float4 *>(a.scores + (size_t)(kvh * kvm + min(hh, kvm - 1)) * S);
+#pragma unroll
+        for (int k = 0; k < PV_SREG; ++k) sreg[hh][k] = sc[min(tid + PV_THREADS * k, S / 4 - 1)];
+    }
+    // V chunk loads: item -> (position t, 8-dim segment sg), the two segments of
+    // a row on adjacent lanes (a wave load covers 32 rows x 32 bytes)
     u32x4 vr[PV_ITEMS];
     auto load_chunk = [&](int t0) {
 #pragma unroll
         for (int it = 0; it < PV_ITEMS; ++it) {
-            const int item = it * PV_THREADS + tid;
-            const int sg = item / PV_TC, t = t0 + item % PV_TC;
+            const int item = it * PV_THREADS + tid, sg = item & 1, t = t0 + (item >> 1);
             vr[it] = *reinterpret_cast<const u32x4 *>(vc + (size_t)min(t, n - 1) * ATT_HD + sg * 8);
         }
     };
     auto store_chunk = [&]() {
 #pragma unroll
         for (int it = 0; it < PV_ITEMS; ++it) {
-            const int item = it * PV_THREADS + tid;
-            const int sg = item / PV_TC, t = item % PV_TC;
+            const int item = it * PV_THREADS + tid, sg = item & 1, t = item >> 1;
             const uint32_t w[4] = {vr[it].x, vr[it].y, vr[it].z, vr[it].w};
 #pragma unroll
             for (int i = 0; i < 8; ++i)
                 vt[(sg * 8 + i) * PV_RS + t] = h2f((uint16_t)(w[i >> 1] >> (16 * (i & 1))));
         }
     };
+    __builtin_amdgcn_sched_barrier(0);
     load_chunk(0);
+    __builtin_amdgcn_sched_barrier(0);
 
-    // scores of this thread's positions t = tid + PV_THREADS*k, k < PV_SREG
-    float sreg[3][PV_SREG];
-#pragma unroll
-    for (int hh = 0; hh < 3; ++hh) {
-        if (hh < kvm) {
-            const float *sc = a.scores + (size_t)(kvh * kvm + hh) * S;
-#pragma unroll
-            for (int k = 0; k < PV_SREG; ++k) sreg[hh][k] = sc[min(tid + PV_THREADS * k, n - 1)];
-        }
-    }
-    // maxima from the chunk maxima, one wave per head
-    const int nch = (n + ATT_CH - 1) / ATT_CH;
+    // ---- M per head from the chunk maxima (beyond one pass: loop)
     if (wid < kvm) {
-        const int h = kvh * kvm + wid;
-        float m = -INFINITY;
-        for (int c = lane; c < nch; c += 64) m = fmaxf(m, a.cmax[h * a.max_chunks + c]);
+        const float *cmh = a.cmax + (kvh * kvm + wid) * a.max_chunks;
+        float m = cm;  // loaded for head wh == wid
+        for (int c = lane + 64; c < nch; c += 64) m = fmaxf(m, cmh[c]);
 #pragma unroll
         for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
         if (lane == 0) hmax[wid] = m;
     }
     lds_barrier();
-    // e_t (text_layer.cpp:486-493, 501-509), stored both ways
+    // ---- e_t (text_layer.cpp:486-493, 501-509), stored both ways, computed
+    // and selected without per-position branches
 #pragma unroll
     for (int hh = 0; hh < 3; ++hh) {
-        if (hh < kvm) {
-            const float M = hmax[hh];
-            const bool fin = __builtin_isfinite(M);
-            float *eh = e + hh * S, *eth = et + hh * 8 * ets;
-            auto put = [&](int t, float v) {
-                const float ev = (fin && v > -INFINITY) ? exp256(v - M) : 0.0f;
-                eh[t] = ev;
-                if (t < nb) eth[(t & 7) * ets + (t >> 3)] = ev;
-            };
-            // zeros after the lane sums' last term, up to a whole batch of 32
-            // per lane: adding +0 to a sum of non-negative terms is exact
-            const int zend = (nb + 255) & ~255;
-            for (int t = nb + tid; t < zend; t += PV_THREADS) eth[(t & 7) * ets + (t >> 3)] = 0.0f;
-#pragma unroll
-            for (int k = 0; k < PV_SREG; ++k) {
-                const int t = tid + PV_THREADS * k;
-                if (t < n) put(t, sreg[hh][k]);
+        if (hh >= kvm) break;  // uniform
+        const float M = hmax[hh];
+        const bool fin = __builtin_isfinite(M);
+        float *eh = e + hh * S, *eth = et + hh * 8 * ets;
+        auto ev_of = [&](float v) {
+            const float x = exp256(v - M);
+            return (fin && v > -INFINITY) ? x : 0.0f;
+        };
+        auto put4 = [&](int t, float4 v) {  // positions t..t+3, t % 4 == 0
+            float4 ev;
+            ev.x = ev_of(v.x);
+            ev.y = ev_of(v.y);
+            ev.z = ev_of(v.z);
+            ev.w = ev_of(v.w);
+            if (t < n) *reinterpret_cast<float4 *>(eh + t) = ev;  // t + 3 < S
+            if (t < nb) {  // nb % 8 == 0: all four below nb
+                const int c = t >> 3, j = t & 7;
+                eth[(j + 0) * ets + c] = ev.x;
+                eth[(j + 1) * ets + c] = ev.y;
+                eth[(j + 2) * ets + c] = ev.z;
+                eth[(j + 3) * ets + c] = ev.w;
             }
-            const float *sc = a.scores + (size_t)(kvh * kvm + hh) * S;
-            for (int t = tid + PV_THREADS * PV_SREG; t < n; t += PV_THREADS) put(t, sc[t]);
-        }
+        };
+        // zeros after the lane sums' last term, up to a whole batch of 32
+        // per lane: adding +0 to a sum of non-negative terms is exact
+        const int zend = (nb + 255) & ~255;
+        for (int t = nb + tid; t < zend; t += PV_THREADS) eth[(t & 7) * ets + (t >> 3)] = 0.0f;
+#pragma unroll
+        for (int k = 0; k < PV_SREG; ++k)
+            if (k < kreg) put4(4 * (tid + PV_THREADS * k), sreg[hh][k]);
+        const float4 *sc = reinterpret_cast<const float4 *>(a.scores + (size_t)(kvh * kvm + hh) * S);
+        for (int i = tid + PV_THREADS * PV_SREG; 4 * i < n; i += PV_THREADS) put4(4 * i, sc[i]);
     }
-    store_chunk();  // V chunk 0 (its loads were issued at entry)
     lds_barrier();
-    // sums and the fp32 inverse, lanes 0..7 of one wave per head
+    // ---- sums and the fp32 inverse, lanes 0..7 of one wave per head; the
+    // other waves widen V chunk 0 into LDS meanwhile
     if (wid < kvm) {
         const float *row = et + wid * 8 * ets + (lane & 7) * ets;
         const int cnt = ((nb >> 3) + 31) & ~31;  // terms per lane, zero-padded
+        const float *eh = e + wid * S;
+        // the tail e_nb .. e_pos (at most 7), one per lane
+        const float tl = lane < n - nb ? eh[nb + lane] : 0.0f;
         float ls = 0.0f;
         if (lane < 8 && cnt > 0) {
             float4 A[8], B[8];
@@ -356,13 +468,25 @@ __global__ __launch_bounds__(PV_THREADS) void attn_softmax_pv_kernel(AttnArgs a)
             ld(A, 0);
             int i = 0;
             for (; i + 64 <= cnt; i += 64) {
-                ld(B, i + 32);
+                lgkm_wait0();  // A has landed; B's reads go out between A's adds
                 __builtin_amdgcn_sched_barrier(0);
+                ld(B, i + 32);
                 add(A);
+#pragma unroll
+                for (int g = 0; g < 8; ++g) {
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+                    __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // four adds
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                lgkm_wait0();
                 __builtin_amdgcn_sched_barrier(0);
                 ld(A, min(i + 64, cnt - 32));
-                __builtin_amdgcn_sched_barrier(0);
                 add(B);
+#pragma unroll
+                for (int g = 0; g < 8; ++g) {
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
+                    __builtin_amdgcn_sched_group_barrier(0x002, 4, 1);
+                }
                 __builtin_amdgcn_sched_barrier(0);
             }
             if (i < cnt) add(A);  // one batch of 32 left
@@ -370,90 +494,82 @@ __global__ __launch_bounds__(PV_THREADS) void attn_softmax_pv_kernel(AttnArgs a)
         double sum = 0.0;
 #pragma unroll
         for (int l = 0; l < 8; ++l) sum += (double)readlane_f(ls, l);
-        const float *eh = e + wid * S;
-        for (int t = nb; t < n; ++t) sum += (double)eh[t];
+#pragma unroll
+        for (int l = 0; l < 7; ++l)
+            if (l < n - nb) sum += (double)readlane_f(tl, l);
         const bool ok = __builtin_isfinite(hmax[wid]) && sum > 0.0 && __builtin_isfinite(sum);
         const float inv = ok ? (float)(1.0 / sum) : 0.0f;
         if (lane == 0) hinv[wid] = inv;
     }
-    lds_barrier();
-    // p_t = e_t * inv, in place (four positions per thread per pass, reads first)
-    for (int hh = 0; hh < kvm; ++hh) {
-        const float inv = hinv[hh];
-        float *eh = e + hh * S;
-        for (int t0 = 0; t0 < n; t0 += 4 * PV_THREADS) {
-            float v[4];
-#pragma unroll
-            for (int k = 0; k < 4; ++k) v[k] = eh[min(t0 + tid + k * PV_THREADS, n - 1)];
-#pragma unroll
-            for (int k = 0; k < 4; ++k)
-                if (t0 + tid + k * PV_THREADS < n) eh[t0 + tid + k * PV_THREADS] = v[k] * inv;
-        }
-    }
+    store_chunk();  // V chunk 0 (its loads were issued at entry)
 
-    // value-weighted sums: lane (ch_h, ch_d) of wave 0 runs one chain
-    const int ch_d = tid % PV_D, ch_h = tid / PV_D;
-    const bool chain = ch_h < kvm;
+    // ---- value-weighted sums. Wave 0 runs the chains: row r of 16 lanes is
+    // query head r, lane d of the row output dim db*PV_D + d. Per batch of 64
+    // positions tb..tb+63, lane k of a row holds p_{tb+4k+c} = e * inv
+    // (c < 4, formed in registers; 0 past the context, which leaves the
+    // chain unchanged: acc is never -0, and fma(0, v, acc) = acc for finite
+    // v) and every step broadcasts one of them across the row.
+    const int rl = lane & 15, hrow = min(lane >> 4, kvm - 1);
+    const bool chain = wid == 0 && (lane >> 4) < kvm;
     float acc = 0.0f;
     for (int t0 = 0; t0 < n; t0 += PV_TC) {
         if (t0 > 0) {
             lds_barrier();  // previous chains done with vt
             store_chunk();
         }
-        lds_barrier();      // vt and p ready
+        lds_barrier();      // vt (and inv) ready
         if (t0 + PV_TC < n) load_chunk(t0 + PV_TC);
         if (chain) {
-            const float *ph = e + ch_h * S + t0;
-            const float *vrow = vt + ch_d * PV_RS;
+            const float invh = hinv[hrow];
+            const float *eph = e + hrow * S + t0;
+            const float *vrow = vt + rl * PV_RS;
             const int len = min(PV_TC, n - t0);
-            int t = 0;
-            if (len >= 32) {
-                // batches of 32 positions in two register sets used in turn:
-                // the next batch's LDS reads are issued before the current
-                // batch's FMAs (all reads < len), with no register copies
-                float4 Av[8], Ap[8], Bv[8], Bp[8];
-                auto ld = [&](float4 *V, float4 *P, int i) {
+            float4 Ae, Be, Av[16], Bv[16];
+            auto ld = [&](float4 &E, float4 *V, int tb) {
+                E = *reinterpret_cast<const float4 *>(eph + tb + 4 * rl);
 #pragma unroll
-                    for (int u = 0; u < 8; ++u) {
-                        V[u] = *reinterpret_cast<const float4 *>(vrow + i + 4 * u);
-                        P[u] = *reinterpret_cast<const float4 *>(ph + i + 4 * u);
-                    }
-                };
-                auto fma32 = [&](const float4 *V, const float4 *P) {
+                for (int u = 0; u < 16; ++u) V[u] = *reinterpret_cast<const float4 *>(vrow + tb + 4 * u);
+            };
+            auto run64 = [&](const float4 &E, const float4 *V, int tb) {
+                const int t = tb + 4 * rl;
+                const float p0 = t + 0 < len ? E.x * invh : 0.0f;
+                const float p1 = t + 1 < len ? E.y * invh : 0.0f;
+                const float p2 = t + 2 < len ? E.z * invh : 0.0f;
+                const float p3 = t + 3 < len ? E.w * invh : 0.0f;
+                asm volatile("s_nop 1" ::"v"(p0), "v"(p1), "v"(p2), "v"(p3));  // DPP read-after-write
 #pragma unroll
-                    for (int u = 0; u < 8; ++u) {
-                        acc = fmaf(P[u].x, V[u].x, acc);
-                        acc = fmaf(P[u].y, V[u].y, acc);
-                        acc = fmaf(P[u].z, V[u].z, acc);
-                        acc = fmaf(P[u].w, V[u].w, acc);
-                    }
-                };
-                ld(Av, Ap, 0);
-                for (; t + 64 <= len; t += 64) {
-                    ld(Bv, Bp, t + 32);
-                    __builtin_amdgcn_sched_barrier(0);
-                    fma32(Av, Ap);
-                    __builtin_amdgcn_sched_barrier(0);
-                    ld(Av, Ap, min(t + 64, (len - 32) & ~3));
-                    __builtin_amdgcn_sched_barrier(0);
-                    fma32(Bv, Bp);
-                    __builtin_amdgcn_sched_barrier(0);
-                }
-                if (t + 32 <= len) {  // A holds positions t .. t+31
-                    fma32(Av, Ap);
-                    t += 32;
-                }
+                for (int k = 0; k < 16; ++k) fmac4_row_bcast(acc, p0, p1, p2, p3, V[k], k);
+            };
+            // batches of 64 in two register sets used in turn: the next
+            // batch's LDS reads are issued before the current batch's steps
+            const int nbat = (len + 63) >> 6;
+            ld(Ae, Av, 0);
+            int bi = 0;
+            for (; bi + 2 <= nbat; bi += 2) {
+                lgkm_wait0();
+                __builtin_amdgcn_sched_barrier(0);
+                ld(Be, Bv, 64 * (bi + 1));
+                run64(Ae, Av, 64 * bi);
+                __builtin_amdgcn_sched_barrier(0);
+                lgkm_wait0();
+                __builtin_amdgcn_sched_barrier(0);
+                ld(Ae, Av, 64 * min(bi + 2, nbat - 1));
+                run64(Be, Bv, 64 * (bi + 1));
+                __builtin_amdgcn_sched_barrier(0);
             }
-            for (; t < len; ++t) acc = fmaf(ph[t], vrow[t], acc);
+            if (bi < nbat) {  // A holds the last batch
+                lgkm_wait0();
+                run64(Ae, Av, 64 * bi);
+            }
         }
     }
-    if (chain) a.out[(kvh * kvm + ch_h) * ATT_HD + db * PV_D + ch_d] = acc;
+    if (chain) a.out[(kvh * kvm + hrow) * ATT_HD + db * PV_D + rl] = acc;
 }
 
 // ------------------------------------------------------------------ launch
 hipError_t launch_embed(const int8_t *w, const float *s, const int32_t *token, float *x, int H,
-                        int gs, hipStream_t st) {
-    embed_kernel<<<(H + 255) / 256, 256, 0, st>>>(w, s, token, x, H, gs);
+                        int gs, int vocab, hipStream_t st) {
+    embed_kernel<<<(H + 255) / 256, 256, 0, st>>>(w, s, token, x, H, gs, vocab);
     return hipGetLastError();
 }
 
@@ -465,11 +581,11 @@ size_t attention_lds_bytes(int heads, int kv_heads, int max_seq) {
 hipError_t launch_attention(const AttnArgs &a, hipStream_t st) {
     const int kvm = a.heads / a.kv_heads;
     if (a.head_dim != ATT_HD || a.heads % a.kv_heads != 0 || kvm < 1 || kvm > 3 ||
-        a.max_seq % 8 != 0)
+        a.max_seq % 8 != 0 || a.max_chunks * ATT_CH < a.max_seq)
         return hipErrorInvalidValue;
     const size_t lds = attention_lds_bytes(a.heads, a.kv_heads, a.max_seq);
     if (lds > kAttnMaxLds) return hipErrorInvalidValue;
-    attn_scores_kernel<<<dim3(a.kv_heads, a.max_chunks), 64 * (kvm + 1), 0, st>>>(a);
+    attn_scores_kernel<<<dim3(a.kv_heads, a.max_chunks), ATT_THREADS, 0, st>>>(a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     static int lds_set = 0;  // raise the dynamic LDS limit once per process

@@ -83,13 +83,15 @@ struct AttnArgs {
     int layer, heads, kv_heads, head_dim, max_seq, max_chunks, gs;
     float eps, inv_sqrt_d;
 };
+// Embedding row of *token (a NaN row for a token outside [0, vocab)).
 hipError_t launch_embed(const int8_t *w, const float *s, const int32_t *token, float *x, int H,
-                        int gs, hipStream_t st);
+                        int gs, int vocab, hipStream_t st);
 hipError_t launch_attention(const AttnArgs &a, hipStream_t st);
 constexpr int kAttnChunk = 64;  // positions per attention score chunk
-// LDS the softmax/value kernel needs; at most kAttnMaxLds.
+// Dynamic LDS the softmax/value kernel needs; at most kAttnMaxLds (160 KiB
+// less room for its static LDS).
 size_t attention_lds_bytes(int heads, int kv_heads, int max_seq);
-constexpr size_t kAttnMaxLds = 160 * 1024 - 256;
+constexpr size_t kAttnMaxLds = 160 * 1024 - 4096;
 
 // ---------------------------------------------------------- GEMM (MFMA)
 struct GemmArgs {
