@@ -309,7 +309,7 @@ __global__ __launch_bounds__(256, 2) void gemm_i8_kernel(GemmArgs a) {
 // * Tile (32*MT*2) x (32*NT*2), 4 waves in 2x2, each wave (32*MT) x (32*NT);
 //   the host picks MT/NT so the grid fills the device. SWIGLU (NT = 2): the
 //   block's B rows 0..63 are gate rows, 64..127 the same up rows.
-template <int MT, int NT, bool SWIGLU>
+template <int MT, int NT, bool SWIGLU, int D>
 __global__ __launch_bounds__(256, 2) void gemm_g64_kernel(GemmArgs a) {
     constexpr int TBM = 64 * MT, TBN = 64 * NT;
     constexpr int ASTG = TBM * 128, BSTG = TBN * 128;  // bytes per stage (fp16)
@@ -356,38 +356,45 @@ __global__ __launch_bounds__(256, 2) void gemm_g64_kernel(GemmArgs a) {
     }
     // scale loaders: thread t < TBM loads a_s of row t, TBM <= t < SCW loads
     // w_s of column t - TBM
+    // (one unconditional load per thread and K-step: base + kb * stride;
+    // threads past SCW read a_s[0] and discard it)
     const bool sc_a = tid < TBM, sc_b = tid >= TBM && tid < SCW;
-    int sc_src = 0;
-    const float *sc_w = nullptr;
-    if (sc_a) sc_src = min(m0 + tid, M - 1);
+    const float *sc_base = a.a_s;
+    int sc_stride = 0;
+    if (sc_a) {
+        sc_base = a.a_s + min(m0 + tid, M - 1);
+        sc_stride = a.lda_s;
+    }
     if (sc_b) {
         const int c = tid - TBM;
         const bool up = SWIGLU && c >= 64;
-        sc_w = up ? a.S1 : a.S0;
-        sc_src = min(n0 + (SWIGLU ? (c & 63) : c), N - 1) * Kg;
+        sc_base = (up ? a.S1 : a.S0) + (size_t)min(n0 + (SWIGLU ? (c & 63) : c), N - 1) * Kg;
+        sc_stride = 1;
     }
 
-    // Global loads of K-step kb+1 are in flight during step kb.
-    u32x4 ra[ACH], rb[BCH];
-    float rs = 0.0f;
-    auto load_regs = [&](int kb) {
+    // Global loads run D K-steps ahead through a ring of D register sets
+    // (slot = K-step % D; the loop below is unrolled D times so every slot
+    // index is a constant). Step kb's slot is free once step kb has been
+    // written to LDS, at the end of iteration kb - 1.
+    u32x4 ra[D][ACH], rb[D][BCH];
+    float rs[D];
+    auto load_regs = [&](int slot, int kb) {
         const int k0 = kb * 64;
 #pragma unroll
-        for (int i = 0; i < ACH; ++i) ra[i] = *reinterpret_cast<const u32x4 *>(a.Aq + a_off[i] + k0);
+        for (int i = 0; i < ACH; ++i) ra[slot][i] = *reinterpret_cast<const u32x4 *>(a.Aq + a_off[i] + k0);
 #pragma unroll
         for (int i = 0; i < BCH; ++i) {
             const int8_t *W = b_up[i] ? a.W1 : a.W0;
-            rb[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(W + b_off[i] + k0));
+            rb[slot][i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(W + b_off[i] + k0));
         }
-        if (sc_a) rs = a.a_s[(size_t)kb * a.lda_s + sc_src];
-        if (sc_b) rs = sc_w[sc_src + kb];
+        rs[slot] = sc_base[(size_t)kb * sc_stride];
     };
-    auto store_lds = [&](int buf, int kb) {
+    auto store_lds = [&](int buf, int slot, int kb) {
 #pragma unroll
-        for (int i = 0; i < ACH; ++i) *reinterpret_cast<u32x4 *>(As(buf) + a_dst[i]) = ra[i];
+        for (int i = 0; i < ACH; ++i) *reinterpret_cast<u32x4 *>(As(buf) + a_dst[i]) = ra[slot][i];
 #pragma unroll
         for (int i = 0; i < BCH; ++i) {
-            u32x4 v = rb[i] ^ (u32x4){0x80808080u, 0x80808080u, 0x80808080u, 0x80808080u};
+            u32x4 v = rb[slot][i] ^ (u32x4){0x80808080u, 0x80808080u, 0x80808080u, 0x80808080u};
             uint32_t w[8];
             widen4(v.x, w[0], w[1]);
             widen4(v.y, w[2], w[3]);
@@ -396,7 +403,7 @@ __global__ __launch_bounds__(256, 2) void gemm_g64_kernel(GemmArgs a) {
             *reinterpret_cast<u32x4 *>(Bs(buf) + b_dst0[i]) = (u32x4){w[0], w[1], w[2], w[3]};
             *reinterpret_cast<u32x4 *>(Bs(buf) + b_dst1[i]) = (u32x4){w[4], w[5], w[6], w[7]};
         }
-        if (tid < SCW) scr[(kb % 3) * SCW + tid] = rs;
+        if (tid < SCW) scr[(kb % 3) * SCW + tid] = rs[slot];
     };
 
     float16_t acc[MT][NT], out[MT][NT];
@@ -466,16 +473,24 @@ __global__ __launch_bounds__(256, 2) void gemm_g64_kernel(GemmArgs a) {
     };
 
     const int nkb = K / 64;
-    load_regs(0);
-    store_lds(0, 0);
+    load_regs(0, 0);
+    store_lds(0, 0, 0);
+#pragma unroll
+    for (int j = 1; j < D; ++j) load_regs(j, min(j, nkb - 1));
     __syncthreads();
-    for (int kb = 0; kb < nkb; ++kb) {
-        const int buf = kb & 1;
-        if (kb + 1 < nkb) load_regs(kb + 1);
-        mfma_step(buf, acc);
-        epilogue(kb, acc);
-        if (kb + 1 < nkb) store_lds(buf ^ 1, kb + 1);
-        __syncthreads();
+    for (int kb0 = 0; kb0 < nkb; kb0 += D) {
+#pragma unroll
+        for (int j = 0; j < D; ++j) {
+            const int kb = kb0 + j;
+            if (kb >= nkb) break;  // uniform
+            // unconditional (the last K-step is reloaded near the end), so
+            // the compiler's load counts do not depend on the path taken
+            load_regs(j, min(kb + D, nkb - 1));
+            mfma_step(kb & 1, acc);
+            epilogue(kb, acc);
+            if (kb + 1 < nkb) store_lds((kb + 1) & 1, (j + 1) % D, kb + 1);
+            __syncthreads();
+        }
     }
 
     // ---- store
@@ -501,18 +516,20 @@ __global__ __launch_bounds__(256, 2) void gemm_g64_kernel(GemmArgs a) {
 
 template <int MT, int NT, bool SWIGLU>
 static hipError_t launch_g64(const GemmArgs &a, hipStream_t st) {
+    // register prefetch depth: as deep as the tile's registers allow
+    constexpr int D = MT * NT >= 4 ? 1 : (MT * NT == 2 ? 3 : 4);
     constexpr int TBM = 64 * MT, TBN = 64 * NT;
     const int ncols = SWIGLU ? TBN / 2 : TBN;
     dim3 grid((a.N + ncols - 1) / ncols, (a.M + TBM - 1) / TBM);
     const size_t lds = 2 * (TBM + TBN) * 128 + 3 * (TBM + TBN) * 4;
     static bool attr_set = false;  // raise the dynamic LDS limit once
     if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemm_g64_kernel<MT, NT, SWIGLU>),
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemm_g64_kernel<MT, NT, SWIGLU, D>),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
         attr_set = true;
     }
-    gemm_g64_kernel<MT, NT, SWIGLU><<<grid, 256, lds, st>>>(a);
+    gemm_g64_kernel<MT, NT, SWIGLU, D><<<grid, 256, lds, st>>>(a);
     return hipGetLastError();
 }
 
