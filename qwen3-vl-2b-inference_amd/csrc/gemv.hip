@@ -100,9 +100,19 @@ __global__ __launch_bounds__(GEMV_MAX_THREADS) void gemv_kernel(GemvArgs a, int 
     sr.Y0 = a.seg[0].Y; sr.Y1 = a.seg[1].Y; sr.Y2 = a.seg[2].Y;
     sr.G0 = a.seg[0].G; sr.G1 = a.seg[1].G; sr.G2 = a.seg[2].G;
     sr.N0 = a.seg[0].N; sr.N1 = a.seg[1].N; sr.N2 = a.seg[2].N;
+    const float *Ap = a.A;
+    const int8_t *norm_w = a.norm_w;
+    const float *norm_s = a.norm_s;
+    int nseg = a.nseg;
+    // The integer kernel arguments are read here, in the entry batch of
+    // scalar loads: the opaque copies keep the compiler from re-loading them
+    // later (its cost model treats a kernel-argument load as free to repeat),
+    // each re-load a dependent round trip. (Pointers are left alone: an
+    // opaque copy would lose their global address space.)
+    asm volatile("" : "+s"(sr.N0), "+s"(sr.N1), "+s"(sr.N2), "+s"(nseg));
     sr.t1 = (sr.N0 + R - 1) / R;
-    sr.t2 = a.nseg > 2 ? sr.t1 + (sr.N1 + R - 1) / R : 0x7fffffff;
-    if (a.nseg < 2) sr.t1 = 0x7fffffff;
+    sr.t2 = nseg > 2 ? sr.t1 + (sr.N1 + R - 1) / R : 0x7fffffff;
+    if (nseg < 2) sr.t1 = 0x7fffffff;
 
     auto resolve = [&](int tile) {
         Tile t;
@@ -132,13 +142,18 @@ __global__ __launch_bounds__(GEMV_MAX_THREADS) void gemv_kernel(GemvArgs a, int 
     // >= K (activation staging, 4 float4 per thread: 16*nthr words), plus
     // the chain-major copy of the row for a fused norm (8 rows of K/8 + 4),
     // and >= 2*nthr (argmax scratch)
-    const bool has_norm = a.norm_w != nullptr;
+    const bool has_norm = norm_w != nullptr;
     const int nrs = K / 8 + 4;
-    const int stage_need = 16 * nthr + (has_norm ? 8 * nrs : 0);
+    // The staged row keeps 4 floats of padding after every group, so the
+    // threads of a wave, each reading its own group, hit distinct banks.
+    const int xpad = 4 * (16 * nthr / GS);
+    const int stage_need = 16 * nthr + xpad + (has_norm ? 8 * nrs : 0);
     int stage_words = acc_words > stage_need ? acc_words : stage_need;
     int32_t *accb = reinterpret_cast<int32_t *>(smem);
     float *xs = reinterpret_cast<float *>(smem);  // phase 0 only (aliases accb)
-    float *xn = xs + 16 * nthr;                   // [8][nrs]: x[l + 8j] at l*nrs + j
+    float *xn = xs + 16 * nthr + xpad;            // [8][nrs]: x[l + 8j] at l*nrs + j
+    // element e of the staged row (groups padded by 4 floats)
+    auto xpos = [&](int e) { return e + 4 * (e / GS); };
     float *as_l = reinterpret_cast<float *>(smem) + stage_words;  // [M][Kg]
     float *sc_l = as_l + MR * Kg;                                   // [R][ld]
     float *ybuf = sc_l + R * ld;                                    // [MR][R]
@@ -179,7 +194,7 @@ __global__ __launch_bounds__(GEMV_MAX_THREADS) void gemv_kernel(GemvArgs a, int 
 #pragma unroll
         for (int j = 0; j < 8; ++j) qp[m][j] = 0;
         if (m >= M) continue;  // uniform: every thread skips together
-        const float4 *src = reinterpret_cast<const float4 *>(a.A + (size_t)m * K);
+        const float4 *src = reinterpret_cast<const float4 *>(Ap + (size_t)m * K);
         // four float4 per thread cover K/4 <= 4 * nthr (named registers; an
         // array here ends up in scratch memory)
         const int i0 = tid, i1 = tid + nthr, i2 = tid + 2 * nthr, i3 = tid + 3 * nthr;
@@ -188,22 +203,22 @@ __global__ __launch_bounds__(GEMV_MAX_THREADS) void gemv_kernel(GemvArgs a, int 
         const float4 x2 = src[i2 < K / 4 ? i2 : 0];
         const float4 x3 = src[i3 < K / 4 ? i3 : 0];
         // fused norm: this thread's 16 weight bytes and group scale
-        u32x4 nw = (u32x4){0u, 0u, 0u, 0u};
-        float nsc = 0.0f;
-        if (has_norm) {
-            nw = *reinterpret_cast<const u32x4 *>(a.norm_w + 16 * (act ? tid : 0));
-            nsc = a.norm_s[act ? (16 * tid) / GS : 0];
-        }
+        // (loaded unconditionally, from the activation row when there is no
+        // norm, so that no later wait depends on which loads were issued)
+        const int8_t *nwp = has_norm ? norm_w : reinterpret_cast<const int8_t *>(Ap);
+        const float *nsp = has_norm ? norm_s : Ap;
+        const u32x4 nw = *reinterpret_cast<const u32x4 *>(nwp + 16 * (act ? tid : 0));
+        const float nsc = nsp[act ? (16 * tid) / GS : 0];
         if (m == 0) prefetch(resolve(tile));  // grid <= ntiles: every block has a tile
         // keep the loads above ahead of the LDS stores below (the stores wait
         // only for the activation loads, issued first); slots past K/4 exist
-        // (stage_words >= 16 * nthr) and are never read
+        // (stage_words >= 16 * nthr + padding) and are never read
         __builtin_amdgcn_sched_barrier(0);
         float4 *xs4 = reinterpret_cast<float4 *>(xs);
-        xs4[i0] = x0;
-        xs4[i1] = x1;
-        xs4[i2] = x2;
-        xs4[i3] = x3;
+        xs4[xpos(4 * i0) / 4] = x0;
+        xs4[xpos(4 * i1) / 4] = x1;
+        xs4[xpos(4 * i2) / 4] = x2;
+        xs4[xpos(4 * i3) / 4] = x3;
         if (has_norm) {
             // chain-major copy: element 4i + c sits in chain 4*(i&1) + c at i/2
             auto put4 = [&](int i, const float4 &v) {
@@ -229,17 +244,44 @@ __global__ __launch_bounds__(GEMV_MAX_THREADS) void gemv_kernel(GemvArgs a, int 
                 if (tid < 8) {
                     const float *row = xn + tid * nrs;
                     const int cnt = K / 8;
-                    int j = 0;
-                    for (; j + 32 <= cnt; j += 32) {
-                        float4 v[8];
+                    // batches of 32 in two register sets used in turn: the
+                    // next batch's reads are in flight during this batch's
+                    // FMAs (s_waitcnt lgkmcnt(0) before issuing them: two
+                    // batches of 8 reads exceed what the 4-bit counter tells
+                    // apart)
+                    float4 A[8], B[8];
+                    auto ld = [&](float4 *D, int i) {
 #pragma unroll
-                        for (int u = 0; u < 8; ++u) v[u] = reinterpret_cast<const float4 *>(row + j)[u];
+                        for (int u = 0; u < 8; ++u) D[u] = reinterpret_cast<const float4 *>(row + i)[u];
+                    };
+                    auto sq = [&](const float4 *D) {
 #pragma unroll
                         for (int u = 0; u < 8; ++u) {
-                            acc = fmaf(v[u].x, v[u].x, acc);
-                            acc = fmaf(v[u].y, v[u].y, acc);
-                            acc = fmaf(v[u].z, v[u].z, acc);
-                            acc = fmaf(v[u].w, v[u].w, acc);
+                            acc = fmaf(D[u].x, D[u].x, acc);
+                            acc = fmaf(D[u].y, D[u].y, acc);
+                            acc = fmaf(D[u].z, D[u].z, acc);
+                            acc = fmaf(D[u].w, D[u].w, acc);
+                        }
+                    };
+                    int j = 0;
+                    if (cnt >= 32) {
+                        ld(A, 0);
+                        for (; j + 64 <= cnt; j += 64) {
+                            __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+                            __builtin_amdgcn_sched_barrier(0);
+                            ld(B, j + 32);
+                            sq(A);
+                            __builtin_amdgcn_sched_barrier(0);
+                            __builtin_amdgcn_s_waitcnt(0xC07F);
+                            __builtin_amdgcn_sched_barrier(0);
+                            ld(A, j + 64 + 32 <= cnt ? j + 64 : j);  // (re-read when no batch is left)
+                            sq(B);
+                            __builtin_amdgcn_sched_barrier(0);
+                        }
+                        if (j + 32 <= cnt) {  // A holds j .. j+31
+                            __builtin_amdgcn_s_waitcnt(0xC07F);
+                            sq(A);
+                            j += 32;
                         }
                     }
                     for (; j < cnt; ++j) acc = fmaf(row[j], row[j], acc);
@@ -255,7 +297,7 @@ __global__ __launch_bounds__(GEMV_MAX_THREADS) void gemv_kernel(GemvArgs a, int 
                 // this thread's 16 elements: x = w * ((s_g * inv) * x)
                 const float comb = nsc * s_norm_inv;
                 const uint32_t wd[4] = {nw.x, nw.y, nw.z, nw.w};
-                float4 *xc4 = reinterpret_cast<float4 *>(xs + 16 * tid);
+                float4 *xc4 = reinterpret_cast<float4 *>(xs + xpos(16 * tid));
 #pragma unroll
                 for (int q4 = 0; q4 < 4; ++q4) {
                     float4 v = xc4[q4];
@@ -273,19 +315,32 @@ __global__ __launch_bounds__(GEMV_MAX_THREADS) void gemv_kernel(GemvArgs a, int 
             // Every thread of a group recomputes the group's sum of squares
             // from LDS in the reference order: 16 FMA chains over the gs/16
             // steps, then the fixed tree.
+            // (all of the group's LDS reads are issued before the first FMA:
+            // one read latency instead of one per pair of reads)
             float P[16];
 #pragma unroll
             for (int i = 0; i < 16; ++i) P[i] = 0.0f;
-            const float *xg = xs + g * GS;
+            const float *xg = xs + g * (GS + 4);
+            constexpr int TB = T < 4 ? T : 4;  // sub-blocks of 16 read per batch
 #pragma unroll
-            for (int t = 0; t < T; ++t) {
+            for (int t0 = 0; t0 < T; t0 += TB) {
+                float4 vb[TB][4];
 #pragma unroll
-                for (int i4 = 0; i4 < 4; ++i4) {
-                    const float4 v = reinterpret_cast<const float4 *>(xg + 16 * t)[i4];
-                    P[4 * i4 + 0] = fmaf(v.x, v.x, P[4 * i4 + 0]);
-                    P[4 * i4 + 1] = fmaf(v.y, v.y, P[4 * i4 + 1]);
-                    P[4 * i4 + 2] = fmaf(v.z, v.z, P[4 * i4 + 2]);
-                    P[4 * i4 + 3] = fmaf(v.w, v.w, P[4 * i4 + 3]);
+                for (int t = 0; t < TB; ++t)
+#pragma unroll
+                    for (int i4 = 0; i4 < 4; ++i4)
+                        vb[t][i4] = reinterpret_cast<const float4 *>(xg + 16 * (t0 + t))[i4];
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int t = 0; t < TB; ++t) {
+#pragma unroll
+                    for (int i4 = 0; i4 < 4; ++i4) {
+                        const float4 v = vb[t][i4];
+                        P[4 * i4 + 0] = fmaf(v.x, v.x, P[4 * i4 + 0]);
+                        P[4 * i4 + 1] = fmaf(v.y, v.y, P[4 * i4 + 1]);
+                        P[4 * i4 + 2] = fmaf(v.z, v.z, P[4 * i4 + 2]);
+                        P[4 * i4 + 3] = fmaf(v.w, v.w, P[4 * i4 + 3]);
+                    }
                 }
             }
             float V[8];
@@ -295,12 +350,12 @@ __global__ __launch_bounds__(GEMV_MAX_THREADS) void gemv_kernel(GemvArgs a, int 
             const float s = group_scale(sumsq, 1.0f / (float)GS);
             const float inv = rcp_rn(s);
             if (tg == 0) as_l[m * Kg + g] = s;
-            const float *xc = xs + 16 * tid;
+            const float4 *xc4 = reinterpret_cast<const float4 *>(xs + xpos(16 * tid));
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int32_t lo = quant_cvt(xc[2 * j] * inv);
-                const int32_t hi = quant_cvt(xc[2 * j + 1] * inv);
-                qp[m][j] = ((uint32_t)lo & 0xFFFFu) | ((uint32_t)hi << 16);
+            for (int q4 = 0; q4 < 4; ++q4) {
+                const float4 v = xc4[q4];
+                qp[m][2 * q4] = quant_pair(v.x * inv, v.y * inv);
+                qp[m][2 * q4 + 1] = quant_pair(v.z * inv, v.w * inv);
             }
         }
         lds_barrier();
@@ -337,9 +392,21 @@ __global__ __launch_bounds__(GEMV_MAX_THREADS) void gemv_kernel(GemvArgs a, int 
                 int32_t p[8];
 #pragma unroll
                 for (int j = 0; j < 8; ++j) p[j] = run_sum<T>(dot2(qp[0][j], wp[j], 0));
-                if (act && tg == 0) {
+                // every thread of the group holds all 8 sums: thread tg writes
+                // 8/T of them (one LDS write instruction per 8/T lanes sums
+                // instead of 8 by the group's first thread)
+                constexpr int WPT = T <= 8 ? 8 / T : 1;
+                if (act && (T <= 8 || tg < 8)) {
 #pragma unroll
-                    for (int j = 0; j < 8; ++j) accb[(r * 8 + j) * ld + g] = p[j] >> 8;
+                    for (int k = 0; k < WPT; ++k) {
+                        const int j = (T <= 8 ? tg * WPT : tg) + k;
+                        int32_t v = p[0];
+#pragma unroll
+                        for (int jj = 1; jj < 8; ++jj) v = jj == j ? p[jj] : v;
+                        accb[(r * 8 + j) * ld + g] = v >> 8;
+                    }
+                }
+                if (act && tg == 0) {
                     if (Gd) {
                         int32_t tot = 0;
 #pragma unroll
@@ -384,14 +451,24 @@ __global__ __launch_bounds__(GEMV_MAX_THREADS) void gemv_kernel(GemvArgs a, int 
                     const int32_t *Lr = accb + tid * ld;
                     const float *scr = sc_l + r * ld;
                     int gg = 0;
-#pragma unroll 2
-                    for (; gg + 4 <= Kg; gg += 4) {
-                        const int4 L4 = *reinterpret_cast<const int4 *>(Lr + gg);
-                        const float4 s4 = *reinterpret_cast<const float4 *>(scr + gg);
-                        c = fmaf((float)L4.x, s4.x, c);  // i8:213-216, groups in order
-                        c = fmaf((float)L4.y, s4.y, c);
-                        c = fmaf((float)L4.z, s4.z, c);
-                        c = fmaf((float)L4.w, s4.w, c);
+                    // batches of 16 groups, every read of a batch issued
+                    // before its FMAs
+                    for (; gg + 16 <= Kg; gg += 16) {
+                        int4 L4[4];
+                        float4 s4[4];
+#pragma unroll
+                        for (int u = 0; u < 4; ++u) {
+                            L4[u] = *reinterpret_cast<const int4 *>(Lr + gg + 4 * u);
+                            s4[u] = *reinterpret_cast<const float4 *>(scr + gg + 4 * u);
+                        }
+                        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                        for (int u = 0; u < 4; ++u) {
+                            c = fmaf((float)L4[u].x, s4[u].x, c);  // i8:213-216, groups in order
+                            c = fmaf((float)L4[u].y, s4[u].y, c);
+                            c = fmaf((float)L4[u].z, s4[u].z, c);
+                            c = fmaf((float)L4[u].w, s4[u].w, c);
+                        }
                     }
                     for (; gg < Kg; ++gg) c = fmaf((float)Lr[gg], scr[gg], c);
                 }
@@ -583,7 +660,7 @@ static hipError_t launch_gemv_t(const GemvArgs &a, int *grid_out, hipStream_t st
     const int nthr = K / 16 > 64 ? K / 16 : 64;
     const int ld = group_ld(Kg);
     const int acc_words = (LANES ? 8 * R : MR * R) * ld;
-    const int stage_need = 16 * nthr + (a.norm_w ? 8 * (K / 8 + 4) : 0);
+    const int stage_need = 16 * nthr + 4 * (16 * nthr / GS) + (a.norm_w ? 8 * (K / 8 + 4) : 0);
     const int stage_words = acc_words > stage_need ? acc_words : stage_need;
     const size_t lds = (size_t)(stage_words + MR * Kg + R * ld + MR * R) * 4;
 

@@ -34,6 +34,16 @@ Q3VL_INLINE int32_t quant_cvt(float p) {
     return v;
 }
 
+// The same for two values, packed as int16 (lo in bits 0..15): the int32 of
+// cvtps2dq is INT32_MIN exactly when !(|p| < 2^31) (NaN, overflow, and
+// p = -2^31 itself, where the rounded value is INT32_MIN anyway), and
+// v_cvt_pk_i16_i32 applies packs_epi32's signed saturation to both.
+Q3VL_INLINE uint32_t quant_pair(float lo, float hi) {
+    const int32_t a = __builtin_fabsf(lo) < 2147483648.0f ? (int32_t)__builtin_rintf(lo) : INT32_MIN;
+    const int32_t b = __builtin_fabsf(hi) < 2147483648.0f ? (int32_t)__builtin_rintf(hi) : INT32_MIN;
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pk_i16(a, b));
+}
+
 // Correctly rounded fp32 sqrt and reciprocal: computed in double and rounded
 // once to fp32. For sqrt and division the double rounding is innocuous
 // (53 >= 2*24+2), so the result equals the IEEE fp32 operation.
