@@ -74,7 +74,10 @@ struct Tile {
     int tseg, tn0, tN;
 };
 
-template <int GS, int MR, bool LANES, int R>
+// KC: the row length K when it is fixed at compile time (the decode step's
+// 2048 and 6144), 0 for a run-time K. With KC set, every quantity derived
+// from K (group count, LDS layout, index divisions) is a constant.
+template <int GS, int MR, bool LANES, int R, int KC>
 __global__ __launch_bounds__(GEMV_MAX_THREADS) void gemv_kernel(GemvArgs a, int ntiles) {
     constexpr int T = GS / 16;
     constexpr int HALF = R / 2;
@@ -83,11 +86,11 @@ __global__ __launch_bounds__(GEMV_MAX_THREADS) void gemv_kernel(GemvArgs a, int 
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ float s_norm_inv;
 
-    const int K = a.K;
+    const int K = KC ? KC : a.K;
     const int Kg = K / GS;
     const int M = a.M;
     const int tid = threadIdx.x;
-    const int nthr = blockDim.x;     // max(K/16, 64)
+    const int nthr = KC ? (KC / 16 > 64 ? KC / 16 : 64) : (int)blockDim.x;  // max(K/16, 64)
     const int nchunk = K / 16;
     const bool act = tid < nchunk;   // owns a 16-byte K-chunk
     const int g = act ? tid / T : 0;
@@ -654,7 +657,7 @@ __global__ void swiglu_kernel(float *gate, const float *up, size_t n) {
 }
 
 // ------------------------------------------------------------------ launch
-template <int GS, int MR, bool LANES, int R>
+template <int GS, int MR, bool LANES, int R, int KC = 0>
 static hipError_t launch_gemv_t(const GemvArgs &a, int *grid_out, hipStream_t st) {
     const int K = a.K, Kg = K / GS;
     const int nthr = K / 16 > 64 ? K / 16 : 64;
@@ -675,7 +678,7 @@ static hipError_t launch_gemv_t(const GemvArgs &a, int *grid_out, hipStream_t st
     if (e != hipSuccess) return e;
     e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
     if (e != hipSuccess) return e;
-    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, gemv_kernel<GS, MR, LANES, R>, nthr, lds);
+    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, gemv_kernel<GS, MR, LANES, R, KC>, nthr, lds);
     if (e != hipSuccess) return e;
     if (occ < 1) occ = 1;
     int grid = cus * occ;
@@ -683,7 +686,7 @@ static hipError_t launch_gemv_t(const GemvArgs &a, int *grid_out, hipStream_t st
     if (grid > ntiles) grid = ntiles;
     if (grid < 1) grid = 1;
     if (grid_out) *grid_out = grid;
-    gemv_kernel<GS, MR, LANES, R><<<grid, nthr, lds, st>>>(a, ntiles);
+    gemv_kernel<GS, MR, LANES, R, KC><<<grid, nthr, lds, st>>>(a, ntiles);
     return hipGetLastError();
 }
 
@@ -705,13 +708,24 @@ static int lane_rows(const GemvArgs &a) {
     return 2;
 }
 
+// The lane path with K fixed at compile time for the decode step's row
+// lengths at group size 64.
+template <int GS, int R>
+static hipError_t launch_lanes(const GemvArgs &a, int *grid_out, hipStream_t st) {
+    if constexpr (GS == 64) {
+        if (a.K == 2048) return launch_gemv_t<GS, 1, true, R, 2048>(a, grid_out, st);
+        if (a.K == 6144) return launch_gemv_t<GS, 1, true, R, 6144>(a, grid_out, st);
+    }
+    return launch_gemv_t<GS, 1, true, R>(a, grid_out, st);
+}
+
 template <int GS>
 static hipError_t launch_gemv_gs(const GemvArgs &a, bool lanes, int *grid_out, hipStream_t st) {
     if (lanes) {
         switch (lane_rows(a)) {
-            case 2: return launch_gemv_t<GS, 1, true, 2>(a, grid_out, st);
-            case 4: return launch_gemv_t<GS, 1, true, 4>(a, grid_out, st);
-            default: return launch_gemv_t<GS, 1, true, 8>(a, grid_out, st);
+            case 2: return launch_lanes<GS, 2>(a, grid_out, st);
+            case 4: return launch_lanes<GS, 4>(a, grid_out, st);
+            default: return launch_lanes<GS, 8>(a, grid_out, st);
         }
     }
     if (a.M <= 1) return launch_gemv_t<GS, 1, false, GEMV_R>(a, grid_out, st);
