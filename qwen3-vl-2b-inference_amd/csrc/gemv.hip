@@ -74,10 +74,26 @@ struct Tile {
     int tseg, tn0, tN;
 };
 
+// Launch kinds with the mode and segment count fixed at compile time.
+// (Plain launches keep the run-time form: fixing their segment count
+// measured slower for q|k|v and down.)
+enum GemvMd : int {
+    MD_RUNTIME = 0,
+    MD_SWIGLU = 1,   // gate|up with the SwiGLU epilogue
+    MD_ARGMAX1 = 2,  // lm_head with the argmax epilogue
+};
+__host__ __device__ constexpr int md_mode(int md) {
+    return md == MD_SWIGLU ? GEMV_SWIGLU : (md == MD_ARGMAX1 ? GEMV_ARGMAX : GEMV_PLAIN);
+}
+__host__ __device__ constexpr int md_nseg(int md) { return md == MD_SWIGLU ? 2 : 1; }
+
 // KC: the row length K when it is fixed at compile time (the decode step's
 // 2048 and 6144), 0 for a run-time K. With KC set, every quantity derived
 // from K (group count, LDS layout, index divisions) is a constant.
-template <int GS, int MR, bool LANES, int R, int KC>
+// MD: the launch's mode and segment count when fixed at compile time
+// (GemvMd), so that segment selection folds away; MD_RUNTIME reads them
+// from the arguments.
+template <int GS, int MR, bool LANES, int R, int KC, int MD>
 __global__ __launch_bounds__(GEMV_MAX_THREADS) void gemv_kernel(GemvArgs a, int ntiles) {
     constexpr int T = GS / 16;
     constexpr int HALF = R / 2;
@@ -95,7 +111,8 @@ __global__ __launch_bounds__(GEMV_MAX_THREADS) void gemv_kernel(GemvArgs a, int 
     const bool act = tid < nchunk;   // owns a 16-byte K-chunk
     const int g = act ? tid / T : 0;
     const int tg = tid % T;
-    const bool swg = a.mode == GEMV_SWIGLU;
+    const int mode = MD == MD_RUNTIME ? a.mode : md_mode(MD);
+    const bool swg = mode == GEMV_SWIGLU;
 
     SegRegs sr;
     sr.W0 = a.seg[0].W; sr.W1 = a.seg[1].W; sr.W2 = a.seg[2].W;
@@ -106,13 +123,14 @@ __global__ __launch_bounds__(GEMV_MAX_THREADS) void gemv_kernel(GemvArgs a, int 
     const float *Ap = a.A;
     const int8_t *norm_w = a.norm_w;
     const float *norm_s = a.norm_s;
-    int nseg = a.nseg;
+    int nseg = MD == MD_RUNTIME ? a.nseg : md_nseg(MD);
     // The integer kernel arguments are read here, in the entry batch of
     // scalar loads: the opaque copies keep the compiler from re-loading them
     // later (its cost model treats a kernel-argument load as free to repeat),
     // each re-load a dependent round trip. (Pointers are left alone: an
     // opaque copy would lose their global address space.)
-    asm volatile("" : "+s"(sr.N0), "+s"(sr.N1), "+s"(sr.N2), "+s"(nseg));
+    asm volatile("" : "+s"(sr.N0), "+s"(sr.N1), "+s"(sr.N2));
+    if constexpr (MD == MD_RUNTIME) asm volatile("" : "+s"(nseg));
     sr.t1 = (sr.N0 + R - 1) / R;
     sr.t2 = nseg > 2 ? sr.t1 + (sr.N1 + R - 1) / R : 0x7fffffff;
     if (nseg < 2) sr.t1 = 0x7fffffff;
@@ -512,7 +530,7 @@ __global__ __launch_bounds__(GEMV_MAX_THREADS) void gemv_kernel(GemvArgs a, int 
         }
 
         // ---- epilogues
-        if (a.mode == GEMV_PLAIN) {
+        if (mode == GEMV_PLAIN) {
             // plain mode: every row of a tile is in segment t.tseg
             if (yvalid) {
                 float *dst = seg_Y(t.tseg) + (size_t)ym * t.tN + row_n(t, yr);
@@ -552,7 +570,7 @@ __global__ __launch_bounds__(GEMV_MAX_THREADS) void gemv_kernel(GemvArgs a, int 
         lds_barrier();
     }
 
-    if (a.mode != GEMV_ARGMAX) return;
+    if (mode != GEMV_ARGMAX) return;
     // ---- argmax: this block's (value, index) partial per activation row, in
     // its own slots (no shared counters or atomics: 2048 blocks contending on
     // one address serialize); argmax_final_kernel reduces the partials.
@@ -657,7 +675,7 @@ __global__ void swiglu_kernel(float *gate, const float *up, size_t n) {
 }
 
 // ------------------------------------------------------------------ launch
-template <int GS, int MR, bool LANES, int R, int KC = 0>
+template <int GS, int MR, bool LANES, int R, int KC = 0, int MD = MD_RUNTIME>
 static hipError_t launch_gemv_t(const GemvArgs &a, int *grid_out, hipStream_t st) {
     const int K = a.K, Kg = K / GS;
     const int nthr = K / 16 > 64 ? K / 16 : 64;
@@ -678,7 +696,7 @@ static hipError_t launch_gemv_t(const GemvArgs &a, int *grid_out, hipStream_t st
     if (e != hipSuccess) return e;
     e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
     if (e != hipSuccess) return e;
-    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, gemv_kernel<GS, MR, LANES, R, KC>, nthr, lds);
+    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, gemv_kernel<GS, MR, LANES, R, KC, MD>, nthr, lds);
     if (e != hipSuccess) return e;
     if (occ < 1) occ = 1;
     int grid = cus * occ;
@@ -686,7 +704,7 @@ static hipError_t launch_gemv_t(const GemvArgs &a, int *grid_out, hipStream_t st
     if (grid > ntiles) grid = ntiles;
     if (grid < 1) grid = 1;
     if (grid_out) *grid_out = grid;
-    gemv_kernel<GS, MR, LANES, R, KC><<<grid, nthr, lds, st>>>(a, ntiles);
+    gemv_kernel<GS, MR, LANES, R, KC, MD><<<grid, nthr, lds, st>>>(a, ntiles);
     return hipGetLastError();
 }
 
@@ -710,11 +728,18 @@ static int lane_rows(const GemvArgs &a) {
 
 // The lane path with K fixed at compile time for the decode step's row
 // lengths at group size 64.
+template <int GS, int R, int KC>
+static hipError_t launch_lanes_k(const GemvArgs &a, int *grid_out, hipStream_t st) {
+    if (a.mode == GEMV_SWIGLU && a.nseg == 2) return launch_gemv_t<GS, 1, true, R, KC, MD_SWIGLU>(a, grid_out, st);
+    if (a.mode == GEMV_ARGMAX && a.nseg == 1) return launch_gemv_t<GS, 1, true, R, KC, MD_ARGMAX1>(a, grid_out, st);
+    return launch_gemv_t<GS, 1, true, R, KC>(a, grid_out, st);
+}
+
 template <int GS, int R>
 static hipError_t launch_lanes(const GemvArgs &a, int *grid_out, hipStream_t st) {
     if constexpr (GS == 64) {
-        if (a.K == 2048) return launch_gemv_t<GS, 1, true, R, 2048>(a, grid_out, st);
-        if (a.K == 6144) return launch_gemv_t<GS, 1, true, R, 6144>(a, grid_out, st);
+        if (a.K == 2048) return launch_lanes_k<GS, R, 2048>(a, grid_out, st);
+        if (a.K == 6144) return launch_lanes_k<GS, R, 6144>(a, grid_out, st);
     }
     return launch_gemv_t<GS, 1, true, R>(a, grid_out, st);
 }
