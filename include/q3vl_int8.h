@@ -154,7 +154,9 @@ int q3vl_swiglu(float *gate, const float *up, size_t n, q3vl_stream stream);
  * [layers, kv_heads, max_seq, head_dim]. `token` and `pos` live in device
  * memory: the call reads the token at position *pos, writes the greedy next
  * token into *token and increments *pos, so a captured HIP graph of one call
- * can be replayed step after step. head_dim must be 128; every linear must
+ * can be replayed step after step. A *pos outside [0, max_seq) leaves the
+ * caches untouched and makes the attention outputs (so the logits) NaN, as
+ * a token outside [0, vocab) does. head_dim must be 128; every linear must
  * take the M=1 lane-ordered GEMV (dimensions >= 1024, <= 8192). */
 typedef struct q3vl_text_model {
     int vocab, hidden, intermediate, layers, heads, kv_heads, head_dim, max_seq, group_size;

@@ -209,6 +209,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_scores_kernel(AttnArgs a) {
     __shared__ __align__(16) uint16_t knew[ATT_HD];
     const int kvh = blockIdx.x, ch = blockIdx.y;
     const int pos = *a.pos;
+    if (pos < 0 || pos >= a.max_seq) return;  // no cache row for it: nothing is touched
     const int n = pos + 1;
     const int t0 = ch * ATT_CH;
     if (t0 >= n) return;  // uniform: chunk past the context
@@ -350,7 +351,13 @@ __global__ __launch_bounds__(PV_THREADS) void attn_softmax_pv_kernel(AttnArgs a)
     __shared__ float hmax[4], hinv[4];
     const int kvh = blockIdx.x, db = blockIdx.y;
     const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63;
-    const int n = *a.pos + 1;
+    const int pos = *a.pos;
+    if (pos < 0 || pos >= S) {  // no cache row for it: NaN outputs
+        if (wid == 0 && (lane >> 4) < kvm)
+            a.out[(kvh * kvm + (lane >> 4)) * ATT_HD + db * PV_D + (lane & 15)] = __builtin_nanf("");
+        return;
+    }
+    const int n = pos + 1;
     const int nb = n & ~7;
     const int nch = (n + ATT_CH - 1) / ATT_CH;
     const uint16_t *vc = a.v_cache + ((size_t)a.layer * a.kv_heads + kvh) * S * ATT_HD + db * PV_D;
@@ -379,11 +386,15 @@ __global__ __launch_bounds__(PV_THREADS) void attn_softmax_pv_kernel(AttnArgs a)
             vr[it] = *reinterpret_cast<const u32x4 *>(vc + (size_t)min(t, n - 1) * ATT_HD + sg * 8);
         }
     };
-    auto store_chunk = [&]() {
+    // rows past pos are stored as zeros (their steps then add exact +0, even
+    // where the row at pos holds an infinity)
+    auto store_chunk = [&](int t0) {
 #pragma unroll
         for (int it = 0; it < PV_ITEMS; ++it) {
             const int item = it * PV_THREADS + tid, sg = item & 1, t = item >> 1;
-            const uint32_t w[4] = {vr[it].x, vr[it].y, vr[it].z, vr[it].w};
+            const bool past = t0 + t > pos;
+            const uint32_t w[4] = {past ? 0u : vr[it].x, past ? 0u : vr[it].y, past ? 0u : vr[it].z,
+                                   past ? 0u : vr[it].w};
 #pragma unroll
             for (int i = 0; i < 8; ++i)
                 vt[(sg * 8 + i) * PV_RS + t] = h2f((uint16_t)(w[i >> 1] >> (16 * (i & 1))));
@@ -501,7 +512,7 @@ __global__ __launch_bounds__(PV_THREADS) void attn_softmax_pv_kernel(AttnArgs a)
         const float inv = ok ? (float)(1.0 / sum) : 0.0f;
         if (lane == 0) hinv[wid] = inv;
     }
-    store_chunk();  // V chunk 0 (its loads were issued at entry)
+    store_chunk(0);  // V chunk 0 (its loads were issued at entry)
 
     // ---- value-weighted sums. Wave 0 runs the chains: row r of 16 lanes is
     // query head r, lane d of the row output dim db*PV_D + d. Per batch of 64
@@ -515,7 +526,7 @@ __global__ __launch_bounds__(PV_THREADS) void attn_softmax_pv_kernel(AttnArgs a)
     for (int t0 = 0; t0 < n; t0 += PV_TC) {
         if (t0 > 0) {
             lds_barrier();  // previous chains done with vt
-            store_chunk();
+            store_chunk(t0);
         }
         lds_barrier();      // vt (and inv) ready
         if (t0 + PV_TC < n) load_chunk(t0 + PV_TC);

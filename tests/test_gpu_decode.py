@@ -26,11 +26,14 @@ def dev():
 class Stepper:
     """Device and oracle copies of one model + caches, stepped together."""
 
-    def __init__(self, dev, orc, dims, seed, ctx, token):
+    def __init__(self, dev, orc, dims, seed, ctx, token, stale_nan=False):
         torch, qm = dev
         self.torch, self.qm, self.orc, self.dims = torch, qm, orc, dims
         self.m = make_text_model(seed, dims)
         k16, v16 = make_kv_cache(seed + 1, dims, ctx)
+        if stale_nan:  # rows at and past ctx hold NaN bits, as an unwritten cache may
+            k16[:, :, ctx:] = np.float16("nan")
+            v16[:, :, ctx:] = np.float16("nan")
         self.ko, self.vo = k16.view(np.uint16).copy(), v16.view(np.uint16).copy()
         self.model = qm.DeviceTextModel(dims, self.m)
         self.kd = torch.from_numpy(k16.view(np.int16).copy()).cuda()
@@ -77,6 +80,35 @@ def test_decode_context_past_one_value_chunk(dev, orc, pos):
     stages V through LDS in chunks of 1024 positions."""
     dims = dict(SMALL, layers=1, max_seq=1280)
     Stepper(dev, orc, dims, seed=40, ctx=pos, token=11).step()
+
+
+@pytest.mark.parametrize("pos", [1000, 2100])
+def test_decode_stale_rows_past_the_context(dev, orc, pos):
+    """Cache rows at and past pos hold NaN bits (never written): the step
+    reads no row past pos into its result and overwrites the row at pos.
+    pos=2100 spans three score passes and three value chunks."""
+    dims = dict(SMALL, layers=1, max_seq=2304)
+    Stepper(dev, orc, dims, seed=45, ctx=pos, token=5, stale_nan=True).step()
+
+
+def test_decode_position_out_of_range(dev):
+    """*pos = max_seq has no cache row: the caches stay as they were and the
+    logits are NaN."""
+    torch, qm = dev
+    dims = dict(SMALL, layers=1, max_seq=256)
+    m = make_text_model(70, dims)
+    k16, v16 = make_kv_cache(71, dims, 256)
+    model = qm.DeviceTextModel(dims, m)
+    kd = torch.from_numpy(k16.view(np.int16).copy()).cuda()
+    vd = torch.from_numpy(v16.view(np.int16).copy()).cuda()
+    tok = torch.tensor([9], dtype=torch.int32, device="cuda")
+    pos = torch.tensor([256], dtype=torch.int32, device="cuda")
+    logits = torch.zeros(dims["vocab"], dtype=torch.float32, device="cuda")
+    qm.decode_step(model, kd, vd, tok, pos, logits, qm.alloc_decode_workspace(model))
+    torch.cuda.synchronize()
+    assert torch.isnan(logits).all()
+    np.testing.assert_array_equal(kd.cpu().numpy(), k16.view(np.int16))
+    np.testing.assert_array_equal(vd.cpu().numpy(), v16.view(np.int16))
 
 
 def test_decode_three_query_heads_per_kv_head(dev, orc):
