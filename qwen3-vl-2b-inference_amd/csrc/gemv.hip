@@ -333,41 +333,74 @@ __global__ __launch_bounds__(GEMV_MAX_THREADS) void gemv_kernel(GemvArgs a, int 
             lds_barrier();
         }
         if (act) {
-            // Every thread of a group recomputes the group's sum of squares
-            // from LDS in the reference order: 16 FMA chains over the gs/16
-            // steps, then the fixed tree.
-            // (all of the group's LDS reads are issued before the first FMA:
-            // one read latency instead of one per pair of reads)
-            float P[16];
+            // The group's sum of squares in the reference order: 16 FMA
+            // chains (chain c takes elements 16t + c over the gs/16 steps t),
+            // V[i] = P[i] + P[i+8], then the fixed tree.
+            float sumsq;
+            if constexpr (T == 4) {
+                // The group's 4 threads are one lane quad; thread tg runs
+                // chains 4tg .. 4tg+3 (one 16-byte read per step). Lanes 0/1
+                // take the P[i+8] of lanes 2/3, and lane 0 takes lane 1's
+                // half of V (DPP quad permutes): the same adds in the same
+                // order, with 4 LDS reads instead of the whole group.
+                const float *xg = xs + g * (GS + 4);
+                float4 cv[4];
 #pragma unroll
-            for (int i = 0; i < 16; ++i) P[i] = 0.0f;
-            const float *xg = xs + g * (GS + 4);
-            constexpr int TB = T < 4 ? T : 4;  // sub-blocks of 16 read per batch
+                for (int t = 0; t < 4; ++t) cv[t] = *reinterpret_cast<const float4 *>(xg + 16 * t + 4 * tg);
+                float p0 = 0.0f, p1 = 0.0f, p2 = 0.0f, p3 = 0.0f;
 #pragma unroll
-            for (int t0 = 0; t0 < T; t0 += TB) {
-                float4 vb[TB][4];
+                for (int t = 0; t < 4; ++t) {
+                    p0 = fmaf(cv[t].x, cv[t].x, p0);
+                    p1 = fmaf(cv[t].y, cv[t].y, p1);
+                    p2 = fmaf(cv[t].z, cv[t].z, p2);
+                    p3 = fmaf(cv[t].w, cv[t].w, p3);
+                }
+#define Q3VL_QUAD(v, ctrl) \
+    __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), ctrl, 0xF, 0xF, false))
+                // quad_perm [2,3,2,3]: lanes 0, 1 read lanes 2, 3
+                const float v0 = p0 + Q3VL_QUAD(p0, 0xEE), v1 = p1 + Q3VL_QUAD(p1, 0xEE);
+                const float v2 = p2 + Q3VL_QUAD(p2, 0xEE), v3 = p3 + Q3VL_QUAD(p3, 0xEE);
+                // quad_perm [1,1,1,1]: lane 1's V[4..7]
+                const float w0 = Q3VL_QUAD(v0, 0x55), w1 = Q3VL_QUAD(v1, 0x55);
+                const float w2 = Q3VL_QUAD(v2, 0x55), w3 = Q3VL_QUAD(v3, 0x55);
+                // lane 0's value to the quad (quad_perm [0,0,0,0])
+                sumsq = Q3VL_QUAD(tree8(v0, v1, v2, v3, w0, w1, w2, w3), 0x00);
+#undef Q3VL_QUAD
+            } else {
+                // every thread of the group runs all 16 chains from LDS (all
+                // of the group's reads are issued before the first FMA: one
+                // read latency instead of one per pair of reads)
+                float P[16];
 #pragma unroll
-                for (int t = 0; t < TB; ++t)
+                for (int i = 0; i < 16; ++i) P[i] = 0.0f;
+                const float *xg = xs + g * (GS + 4);
+                constexpr int TB = T < 4 ? T : 4;  // sub-blocks of 16 read per batch
 #pragma unroll
-                    for (int i4 = 0; i4 < 4; ++i4)
-                        vb[t][i4] = reinterpret_cast<const float4 *>(xg + 16 * (t0 + t))[i4];
-                __builtin_amdgcn_sched_barrier(0);
+                for (int t0 = 0; t0 < T; t0 += TB) {
+                    float4 vb[TB][4];
 #pragma unroll
-                for (int t = 0; t < TB; ++t) {
+                    for (int t = 0; t < TB; ++t)
 #pragma unroll
-                    for (int i4 = 0; i4 < 4; ++i4) {
-                        const float4 v = vb[t][i4];
-                        P[4 * i4 + 0] = fmaf(v.x, v.x, P[4 * i4 + 0]);
-                        P[4 * i4 + 1] = fmaf(v.y, v.y, P[4 * i4 + 1]);
-                        P[4 * i4 + 2] = fmaf(v.z, v.z, P[4 * i4 + 2]);
-                        P[4 * i4 + 3] = fmaf(v.w, v.w, P[4 * i4 + 3]);
+                        for (int i4 = 0; i4 < 4; ++i4)
+                            vb[t][i4] = reinterpret_cast<const float4 *>(xg + 16 * (t0 + t))[i4];
+                    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                    for (int t = 0; t < TB; ++t) {
+#pragma unroll
+                        for (int i4 = 0; i4 < 4; ++i4) {
+                            const float4 v = vb[t][i4];
+                            P[4 * i4 + 0] = fmaf(v.x, v.x, P[4 * i4 + 0]);
+                            P[4 * i4 + 1] = fmaf(v.y, v.y, P[4 * i4 + 1]);
+                            P[4 * i4 + 2] = fmaf(v.z, v.z, P[4 * i4 + 2]);
+                            P[4 * i4 + 3] = fmaf(v.w, v.w, P[4 * i4 + 3]);
+                        }
                     }
                 }
-            }
-            float V[8];
+                float V[8];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) V[i] = P[i] + P[i + 8];
-            const float sumsq = tree8(V[0], V[1], V[2], V[3], V[4], V[5], V[6], V[7]);
+                for (int i = 0; i < 8; ++i) V[i] = P[i] + P[i + 8];
+                sumsq = tree8(V[0], V[1], V[2], V[3], V[4], V[5], V[6], V[7]);
+            }
             const float s = group_scale(sumsq, 1.0f / (float)GS);
             const float inv = rcp_rn(s);
             if (tg == 0) as_l[m * Kg + g] = s;
