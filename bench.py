@@ -27,7 +27,10 @@ and context, timed on this host's cores for a bounded number of tokens.
 
 Also reported under "configs": config 0 (up_proj GEMV, GB/s), config 2
 (prefill gate|up+SwiGLU and down at M=512, TOPS), config 3 (lm_head GEMV +
-argmax, M=1 and 8, GB/s), config 4 (vision-encoder linears, TOPS).
+argmax, M=1 and 8, GB/s), config 4 (vision-encoder linears, TOPS), the
+exporter's weight quantizer on one up_proj ("export", GB/s) and, with
+--configs ...,load, the load of a full-size checkpoint file into HBM (GB/s of
+file bytes, page-cache-resident file).
 """
 from __future__ import annotations
 
@@ -363,6 +366,78 @@ def bench_cfg4(args):
                 kernel="quantize_rows_kernel + gemm_g64_kernel<MT, NT, SWIGLU, D>")
 
 
+# ------------------------------------------------- checkpoint files
+def bench_export(args):
+    """q3vl_quantize_groupwise over one up_proj [6144, 2048] fp32 at group 64."""
+    import torch
+    import q3vl_int8 as q
+    N, K = 6144, 2048
+    n = copies_for(N * K * 4)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(0xF4)
+    Xs = [torch.randn((N, K), dtype=torch.float32, device="cuda", generator=g) * 0.02
+          for _ in range(n)]
+    qo = torch.empty((N, K), dtype=torch.int8, device="cuda")
+    so = torch.empty((N * K // GS,), dtype=torch.float32, device="cuda")
+    ms = _event_time(lambda i: q.quantize_groupwise(Xs[i % n], GS, qo, so),
+                     max(args.steps, 200), 20)
+    algo = N * K * 4 + N * K + (N * K // GS) * 4
+    gbs = algo / (ms * 1e-3) / 1e9
+    return dict(name="export_quantizer", metric="GB/s", value=gbs, ms=ms, algo_bytes=algo,
+                frac=gbs / HBM_PEAK_GBS, copies=n, kernel="quantize_export_vec_kernel<64, 2>")
+
+
+def bench_load(args):
+    """Loads a full-size (28-layer, vocab 151936, group 64) checkpoint file
+    into HBM with q3vl_checkpoint_load; the file is written first (random
+    int8 values and U(0.001,0.02) scales), so it is page-cache resident."""
+    import tempfile
+
+    import numpy as np
+    from q3vl_int8 import checkpoint as ck
+    hdr = dict(vocab=151936, hidden=2048, intermediate=6144, layers=28, heads=16, kv_heads=8,
+               max_position=262144, rope_theta=5000000, rms_eps=1e-6, vision_hidden=1024,
+               vision_depth=24, vision_patch=16, vision_spatial_merge=2,
+               vision_temporal_patch=2, vision_heads=16, vision_intermediate=4096,
+               out_hidden=2048, image_token_id=151655, vision_start_token_id=151652,
+               vision_end_token_id=151653, video_token_id=151656, text_bits=8,
+               group_size=GS, vision_bits=16, group_quantized=1)
+    spans = ck.text_layout(hdr)
+    rng = np.random.default_rng(0xF1)
+    pool_q = rng.integers(-127, 128, size=64 << 20, dtype=np.int8).tobytes()
+    pool_s = rng.uniform(0.001, 0.02, size=16 << 20).astype(np.float32).tobytes()
+    d = tempfile.mkdtemp()
+    path = os.path.join(d, "qwen3vl_2b_text_i8.bin")
+    try:
+        with open(path, "wb") as f:
+            f.write(ck.pack_header(hdr))
+            for n in ck.TEXT_TENSORS:
+                for nbytes, pool in ((spans[n]["scales_count"] * 4, pool_s),
+                                     (spans[n]["data_count"], pool_q)):
+                    while nbytes:
+                        k = min(nbytes, len(pool))
+                        f.write(pool[:k])
+                        nbytes -= k
+        end = spans["final_norm"]["data_offset"] + spans["final_norm"]["data_count"]
+        text_bytes = end - ck.HEADER_BYTES
+        times = []
+        for _ in range(3):
+            t = time.perf_counter()
+            c = ck.Checkpoint(path, max_seq=4096)
+            times.append(time.perf_counter() - t)
+            c.close()
+        best = min(times)
+    finally:
+        try:
+            os.remove(path)
+        finally:
+            os.rmdir(d)
+    return dict(name="checkpoint_load", metric="GB/s", value=text_bytes / best / 1e9,
+                ms=best * 1e3, text_bytes=text_bytes, runs_s=[round(x, 4) for x in times],
+                note="file bytes / wall time of q3vl_checkpoint_load (allocation, reads from "
+                     "the page cache, host-to-device copies, RoPE tables for 4096 rows)")
+
+
 def cpu_baseline_cfg0(budget_s):
     """The reference's linear() (oracle/_ref) on config 0's shape."""
     import numpy as np
@@ -431,7 +506,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200, help="timed decode steps (tokens)")
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--configs", default="cfg1,cfg0,cfg2,cfg3,cfg4")
+    ap.add_argument("--configs", default="cfg1,cfg0,cfg2,cfg3,cfg4,export")
     ap.add_argument("--cpu-budget", type=float, default=15.0,
                     help="seconds of reference CPU decode for cpu_baseline (0: skip)")
     ap.add_argument("--pmc-workload", action="store_true",
@@ -439,7 +514,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (see the sharding "
-              "notes in DESIGN.md); run with --gpus 1", file=sys.stderr)
+              "notes in the design document); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
     import torch
     import q3vl_int8 as q
@@ -465,6 +540,12 @@ def main():
             results.append(bench_cfg3(args, 8))
         elif c == "cfg4":
             results.append(bench_cfg4(args))
+        elif c == "export":
+            results.append(bench_export(args))
+        elif c == "load":
+            results.append(bench_load(args))
+        else:
+            raise SystemExit(f"unknown config {c!r} (cfg0..cfg4, export, load)")
         torch.cuda.synchronize()
         log(json.dumps(results[-1]))
     by = {r["name"]: r for r in results}

@@ -181,6 +181,86 @@ int q3vl_decode_step(const q3vl_text_model *m, uint16_t *k_cache, uint16_t *v_ca
                      int32_t *token, int32_t *pos, float *logits, void *workspace,
                      size_t workspace_bytes, q3vl_stream stream);
 
+/* ---- checkpoint files: the reference's single-file .bin
+ * (model/src/load_model.cpp:50-246, written by
+ * export_bin/export_qwen_bin.py:212-420). A 100-byte header
+ * (q3vl_checkpoint_header, little-endian int32 / float32), then tensor
+ * groups in a fixed order. An int8 group stores all of its fp32 scales, then
+ * all of its int8 values; an fp16 / fp32 group stores its values. The text
+ * groups, in file order (q3vl_checkpoint_tensor): embed_tokens [vocab,
+ * hidden]; input_layernorm [layers, hidden] (applied before attention: the
+ * reference's rms_ffn_w, forward.cpp:494); mlp down [layers, hidden, inter];
+ * gate, up [layers, inter, hidden]; post_attention_layernorm [layers,
+ * hidden] (before the MLP: rms_attn_w, forward.cpp:612); k_norm [layers,
+ * head_dim]; k [layers, kv_heads*head_dim, hidden]; o [layers, hidden,
+ * hidden]; q_norm; q [layers, heads*head_dim, hidden]; v; the final norm
+ * [hidden]. The vision groups follow. Norm tensors are group-quantized
+ * always; the other int8 tensors when group_quantized != 0, else with one
+ * scale per row. */
+typedef struct q3vl_checkpoint_header {
+    int vocab, hidden, intermediate, layers, heads, kv_heads, max_position, rope_theta;
+    float rms_eps;
+    int vision_hidden, vision_depth, vision_patch, vision_spatial_merge, vision_temporal_patch,
+        vision_heads, vision_intermediate, out_hidden;
+    int image_token_id, vision_start_token_id, vision_end_token_id, video_token_id;
+    int text_bits, group_size, vision_bits, group_quantized;
+} q3vl_checkpoint_header; /* the file's first 100 bytes */
+
+enum q3vl_checkpoint_tensor {
+    Q3VL_CK_EMBED = 0, Q3VL_CK_ATTN_NORM, Q3VL_CK_DOWN, Q3VL_CK_GATE, Q3VL_CK_UP,
+    Q3VL_CK_MLP_NORM, Q3VL_CK_K_NORM, Q3VL_CK_K, Q3VL_CK_O, Q3VL_CK_Q_NORM, Q3VL_CK_Q,
+    Q3VL_CK_V, Q3VL_CK_FINAL_NORM, Q3VL_CK_TEXT_TENSORS
+};
+
+/* One tensor group's place in the file. */
+typedef struct q3vl_checkpoint_span {
+    size_t scales_offset; /* byte offset of the fp32 scales (int8 groups) */
+    size_t scales_count;  /* number of scales (0 for fp16 / fp32 groups) */
+    size_t data_offset;   /* byte offset of the values */
+    size_t data_count;    /* number of values */
+    int bits;             /* 8, 16 or 32 */
+    int group;            /* values per scale (int8 groups) */
+} q3vl_checkpoint_span;
+
+/* The header of a checkpoint file (the field reads of load_model.cpp:62-91).
+ * Host only. Q3VL_ERR_INVALID_ARGUMENT for a missing or short file. */
+int q3vl_checkpoint_read_header(const char *path, q3vl_checkpoint_header *hdr);
+
+/* The text groups' places, spans[Q3VL_CK_TEXT_TENSORS], as map_tensor walks
+ * the file (load_model.cpp:146-195). Host only. */
+int q3vl_checkpoint_text_layout(const q3vl_checkpoint_header *hdr, q3vl_checkpoint_span *spans);
+
+/* RoPE tables for text positions 0..rows-1 (the T section of
+ * qwen_rope_precompute, load_model.cpp:416-490; a text position has its
+ * three sections equal): cos[p][i] = cosf(p * inv_freq[i]),
+ * inv_freq[i] = 1.0f / powf(theta, (2.0f * i) / head_dim), fp32 with the
+ * host's libm. Host only; cos_out and sin_out hold rows * head_dim/2. */
+int q3vl_rope_tables(int rope_theta, int head_dim, int rows, float *cos_out, float *sin_out);
+
+/* A checkpoint's text model in device memory on the current device: one
+ * allocation, every tensor 256-byte aligned, and RoPE tables for max_seq
+ * positions (the device-resident counterpart of init_model_weights and the
+ * run state's tables, load_model.cpp:50-195 and :413-490). Needs int8 text
+ * weights, group-quantized with a group size the decode step serves, and
+ * head_dim 128; Q3VL_ERR_UNSUPPORTED names what does not fit. The copies are
+ * complete when the call returns. */
+typedef struct q3vl_checkpoint q3vl_checkpoint;
+int q3vl_checkpoint_load(const char *path, int max_seq, q3vl_stream stream,
+                         q3vl_checkpoint **out);
+/* The loaded model (valid until q3vl_checkpoint_free). */
+const q3vl_text_model *q3vl_checkpoint_text_model(const q3vl_checkpoint *ck);
+int q3vl_checkpoint_header_of(const q3vl_checkpoint *ck, q3vl_checkpoint_header *hdr);
+void q3vl_checkpoint_free(q3vl_checkpoint *ck);
+
+/* The exporter's weight quantizer on the device (quantize_groupwise,
+ * export_bin/export_qwen_bin.py:260-275): per group of `group` consecutive
+ * values, m = max|x| + 1e-8, s = m / 127 (fp32), q = round half to even of
+ * x / s, clipped to [-127, 127]; scales[i] = s of group i. quantize_rowwise
+ * (:242-258) is the case group = row length. count must be a multiple of
+ * group; x must be finite. Device pointers, asynchronous on `stream`. */
+int q3vl_quantize_groupwise(const float *x, size_t count, size_t group, int8_t *q,
+                            float *scales, q3vl_stream stream);
+
 /* ---- weight registry for host-pointer callers (the drop-in linear()).
  * The reference hands linear() mmapped host pointers to weights and scales
  * (model/src/load_model.cpp:146-181); the registry uploads a weight once and

@@ -181,3 +181,27 @@ int32_t orc_argmax(const float *logits, size_t V) {
 void orc_argmax_rows(const float *logits, size_t M, size_t V, int32_t *ids) {
     for (size_t m = 0; m < M; ++m) ids[m] = orc_argmax(logits + m * V, V);
 }
+
+/* export_bin/export_qwen_bin.py:260-275. numpy evaluates every step in
+ * float32 (the array dtype; the Python scalars 1e-8 and 127 are cast to it):
+ * np.max(np.abs(x)) + 1e-8, maxv / qmax, np.round(x / scales) (half to even,
+ * rintf under the default rounding mode), then np.clip. */
+void orc_quantize_groupwise(const float *x, size_t count, size_t group, int8_t *q,
+                            float *scales) {
+    for (size_t g = 0; g * group < count; ++g) {
+        const float *xg = x + g * group;
+        float m = 0.0f;
+        for (size_t i = 0; i < group; ++i) {
+            const float a = fabsf(xg[i]);
+            if (a > m) m = a;
+        }
+        const float s = (m + 1e-8f) / 127.0f;
+        scales[g] = s;
+        for (size_t i = 0; i < group; ++i) {
+            float r = rintf(xg[i] / s);
+            if (r > 127.0f) r = 127.0f;
+            if (r < -127.0f) r = -127.0f;
+            q[g * group + i] = (int8_t)r;
+        }
+    }
+}

@@ -18,6 +18,11 @@
  *     spike, all-zero group, round-half-even ties) and an int64 brute force.
  *   - argmax: brute force and the tie / NaN / -inf cases of greedy_decode.
  *   - swiglu: against the compiled reference swiglu() (libm expf).
+ *   - quantize_groupwise: closed forms -- groups whose maximum is 127 (g + 1)
+ *     have scale g + 1 exactly and x = k (g + 1) maps to k (so the group
+ *     indexing and sign are pinned), an all-zero group has scale
+ *     fp32(1e-8) / 127 and zeros, and x / s = n + 1/2 rounds to even -- plus the
+ *     bound |q s - x| <= s / 2 on random data.
  */
 #ifndef Q3VL_ORACLE_H
 #define Q3VL_ORACLE_H
@@ -29,32 +34,40 @@
 extern "C" {
 #endif
 
-/* a7: per-row, per-group RMS int16 activation quantizer.
+/* Per-row, per-group RMS int16 activation quantizer
+ * (matmul/src/cpu_f32a_i8f32sb_f32c_avx2.cpp:135-177).
  * A [M,K] fp32 -> q [M,K] int16, a_s [M,K/gs] fp32. */
 void orc_quantize_rows(const float *A, size_t M, size_t K, size_t gs,
                        int16_t *q, float *a_s);
 
-/* a5/a6: M=1 lane-ordered GEMV. G (optional) receives [N,K/gs] int32 sums. */
+/* M=1 lane-ordered GEMV (cpu_f32a_i8f32sb_f32c_avx2.cpp:122-224). G (optional) receives [N,K/gs] int32 sums. */
 void orc_gemv_lanes(const float *x, const int8_t *W, const float *S, float *y,
                     int32_t *G, size_t N, size_t K, size_t gs);
 
-/* a4: general path. contract!=0 evaluates acc = fma(G*a_s, w_s, acc);
+/* General path (cpu_f32a_i8f32sb_f32c_avx2.cpp:477-662). contract!=0 evaluates acc = fma(G*a_s, w_s, acc);
  * contract==0 evaluates acc = acc + (G*a_s)*w_s with three roundings. */
 void orc_linear_general(const float *A, const int8_t *W, const float *S,
                         float *C, int32_t *G, size_t M, size_t N, size_t K,
                         size_t gs, int contract);
 
-/* a4 dispatch: lane path when M==1 && N>=1024 && K>=1024, else general. */
+/* Dispatch (matmul/src/cpu_wrapper.cpp:339-348): lane path when M==1 && N>=1024 && K>=1024, else general. */
 int orc_uses_lane_path(size_t M, size_t N, size_t K);
 void orc_linear_i8(const float *A, const int8_t *W, const float *S, float *C,
                    int32_t *G, size_t M, size_t N, size_t K, size_t gs);
 
-/* a9: gate[i] = (g / (1 + expf(-g))) * up[i], in place on gate. */
+/* swiglu (layers/src/text_layer.cpp:420-434): gate[i] = (g / (1 + expf(-g))) * up[i], in place on gate. */
 void orc_swiglu(float *gate, const float *up, size_t n);
 
-/* a11: greedy_decode argmax over each of M rows of V logits. */
+/* greedy_decode (tokenizer/src/utils.cpp:34-44): argmax over each of M rows of V logits. */
 int32_t orc_argmax(const float *logits, size_t V);
 void orc_argmax_rows(const float *logits, size_t M, size_t V, int32_t *ids);
+
+/* The checkpoint exporter's weight quantizer, quantize_groupwise of
+ * export_bin/export_qwen_bin.py:260-275 (numpy fp32): m = max|x| + 1e-8,
+ * s = m / 127, q = round-half-even(x / s) clipped to [-127, 127].
+ * x [count] -> q [count], scales [count / group]. */
+void orc_quantize_groupwise(const float *x, size_t count, size_t group, int8_t *q,
+                            float *scales);
 
 /* ---- decode step (decode_oracle.c): the int8 path's caller, forward_text */
 typedef struct orc_model {

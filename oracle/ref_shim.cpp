@@ -4,7 +4,9 @@
 // TEST INFRASTRUCTURE ONLY. It lets tests and the golden-vector writer call the
 // reference's real linear() (matmul/src/cpu_wrapper.cpp:308), its text-layer
 // ops (layers/src/text_layer.cpp) and its decode step forward_text()
-// (model/src/forward.cpp:458), and lets bench.py time the reference CPU path.
+// (model/src/forward.cpp:458), its checkpoint loader init_model_weights()
+// (model/src/load_model.cpp:50) and RoPE tables qwen_rope_precompute()
+// (model/src/load_model.cpp:413), and lets bench.py time the reference CPU path.
 // Nothing here is linked into the HIP library.
 #include <fcntl.h>
 #include <unistd.h>
@@ -18,6 +20,7 @@
 #include "layers/include/text_layer.hpp"
 #include "matmul/module.hpp"
 #include "model/include/forward.hpp"
+#include "model/include/load_model.hpp"
 
 namespace {
 
@@ -239,6 +242,93 @@ void ref_decoder_destroy(void *h) {
     auto *r = static_cast<RefDecoder *>(h);
     for (Tensor *t : r->owned) release(t);
     delete r;
+}
+
+// ---- checkpoint loader (model/src/load_model.cpp:50-246)
+struct ref_ck_tensor {
+    const void *data;    // mapped values
+    const void *scales;  // mapped fp32 scales (int8 tensors), else null
+    size_t count;        // values
+    size_t group;        // values per scale (int8 tensors)
+    int dtype;           // DType::Type
+};
+
+struct RefCheckpoint {
+    QwenConfig cfg{};
+    QwenWeight w{};
+};
+
+// Maps a checkpoint with init_model_weights. cfg25 receives the 25 header
+// fields in file order (rms_norm_eps as its float bits); out receives the 13
+// text tensors in file order, then the 27 vision tensors in file order.
+// Returns null when the loader mapped nothing.
+void *ref_checkpoint_open(const char *path, int *cfg25, ref_ck_tensor *out) {
+    Silence quiet;
+    auto *r = new RefCheckpoint();
+    init_model_weights(path, &r->cfg, &r->w);
+    if (!r->w.rms_out_w) {
+        delete r;
+        return nullptr;
+    }
+    const QwenConfig &c = r->cfg;
+    int eps_bits;
+    memcpy(&eps_bits, &c.rms_norm_eps, 4);
+    const int f[25] = {c.vocab_size, c.hidden_size, c.intermediate_size, c.num_hidden_layers,
+                       c.num_attention_heads, c.num_key_value_heads, c.max_position_embeddings,
+                       c.rope_theta, eps_bits, c.vision_hidden_size, c.vision_depth,
+                       c.vision_patch_size, c.vision_spatial_merge_size,
+                       c.vision_temporal_patch_size, c.vision_num_heads,
+                       c.vision_intermediate_size, c.out_hidden_size, c.image_token_id,
+                       c.vision_start_token_id, c.vision_end_token_id, c.video_token_id,
+                       c.text_bits, c.group_size, c.vision_bits, c.group_quantized};
+    memcpy(cfg25, f, sizeof f);
+    const QwenWeight &w = r->w;
+    const Tensor *ts[] = {
+        w.token_embedding_table, w.rms_ffn_w, w.w_mlp_down, w.w_mlp_gate, w.w_mlp_up,
+        w.rms_attn_w, w.w_attn_k_norm, w.w_attn_k, w.w_attn_o, w.w_attn_q_norm, w.w_attn_q,
+        w.w_attn_v, w.rms_out_w,
+        w.vl_patch_emb_b, w.vl_patch_emb_w, w.vl_pos_emb_w, w.vl_attn_proj_b, w.vl_attn_proj_w,
+        w.vl_attn_qkv_b, w.vl_attn_qkv_w, w.vl_mlp1_b, w.vl_mlp1_w, w.vl_mlp2_b, w.vl_mlp2_w,
+        w.vl_norm1_b, w.vl_norm1_w, w.vl_norm2_b, w.vl_norm2_w,
+        w.vl_d_mlp1_b, w.vl_d_mlp1_w, w.vl_d_mlp2_b, w.vl_d_mlp2_w, w.vl_d_norm_b, w.vl_d_norm_w,
+        w.vl_merge_mlp1_b, w.vl_merge_mlp1_w, w.vl_merge_mlp2_b, w.vl_merge_mlp2_w,
+        w.vl_merge_norm_b, w.vl_merge_norm_w};
+    for (size_t i = 0; i < sizeof ts / sizeof ts[0]; ++i) {
+        const Tensor *t = ts[i];
+        out[i].data = t->buf;
+        out[i].scales = t->scale_buf;
+        out[i].count = t->num_elem();
+        out[i].group = t->group_size;
+        out[i].dtype = (int)t->dtype;
+    }
+    return r;
+}
+
+void ref_checkpoint_close(void *h) {
+    auto *r = static_cast<RefCheckpoint *>(h);
+    free_model_weights(&r->w);
+    free_model_config(&r->cfg);
+    delete r;
+}
+
+// qwen_rope_precompute over caller buffers cos3/sin3 [3][seq_len][head_dim/2].
+void ref_rope_precompute(int rope_theta, int hidden, int heads, int seq_len, float *cos3,
+                         float *sin3) {
+    Silence quiet;
+    QwenConfig c{};
+    int sections[3] = {24, 20, 20};  // load_model.cpp:96-98
+    c.seq_len = seq_len;
+    c.hidden_size = hidden;
+    c.num_attention_heads = heads;
+    c.rope_theta = rope_theta;
+    c.mrope_section = sections;
+    c.num_dimensions = 3;
+    const size_t half = (size_t)(hidden / heads) / 2;
+    Tensor *tc = f32({3, (size_t)seq_len, half}, cos3);
+    Tensor *tsn = f32({3, (size_t)seq_len, half}, sin3);
+    qwen_rope_precompute(tc, tsn, &c);
+    release(tc);
+    release(tsn);
 }
 
 }  // extern "C"

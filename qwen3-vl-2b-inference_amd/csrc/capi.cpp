@@ -281,8 +281,8 @@ DecodeLayout decode_layout(const q3vl_text_model *m) {
     return L;
 }
 
-int check_model(const q3vl_text_model *m) {
-    if (!m) return fail(Q3VL_ERR_INVALID_ARGUMENT, "null model");
+// The shapes the decode step serves (no pointers read).
+int check_model_dims(const q3vl_text_model *m) {
     const long H = m->hidden, I = m->intermediate, D = m->head_dim, gs = m->group_size;
     if (D != 128 || m->heads <= 0 || m->kv_heads <= 0 || m->heads % m->kv_heads ||
         m->heads / m->kv_heads > 3)
@@ -301,6 +301,12 @@ int check_model(const q3vl_text_model *m) {
         return fail(Q3VL_ERR_UNSUPPORTED,
                     "max_seq %d too long for the attention kernel's LDS (heads/kv_heads %d)",
                     m->max_seq, m->heads / m->kv_heads);
+    return Q3VL_OK;
+}
+
+int check_model(const q3vl_text_model *m) {
+    if (!m) return fail(Q3VL_ERR_INVALID_ARGUMENT, "null model");
+    if (int rc = check_model_dims(m)) return rc;
     const void *ptrs[] = {m->embed_w, m->embed_s, m->final_norm_w, m->final_norm_s,
                           m->attn_norm_w, m->attn_norm_s, m->mlp_norm_w, m->mlp_norm_s,
                           m->q_norm_w, m->q_norm_s, m->k_norm_w, m->k_norm_s, m->wq, m->wk,
@@ -631,6 +637,304 @@ int q3vl_weight_release_all(void) {
         (void)hipFree(kv.second.dS);
     }
     g_reg.clear();
+    return Q3VL_OK;
+}
+
+}  // extern "C"
+
+// ------------------------------------------------------------ checkpoint files
+struct q3vl_checkpoint {
+    q3vl_checkpoint_header hdr;
+    q3vl_text_model model;
+    void *dev;  // one allocation holding every tensor and the RoPE tables
+    int device;
+};
+
+namespace {
+
+constexpr size_t kCkHeaderBytes = 100;
+static_assert(sizeof(q3vl_checkpoint_header) == kCkHeaderBytes,
+              "the header struct is the file's first 100 bytes");
+
+// map_tensor's walk over the text groups (load_model.cpp:146-195): per group,
+// the scales (int8) then the values; norm tensors always group-quantized.
+int ck_layout(const q3vl_checkpoint_header *h, q3vl_checkpoint_span *sp) {
+    if (!h || !sp) return fail(Q3VL_ERR_INVALID_ARGUMENT, "null header / spans");
+    if (h->vocab <= 0 || h->hidden <= 0 || h->intermediate <= 0 || h->layers <= 0 ||
+        h->heads <= 0 || h->kv_heads <= 0 || h->hidden % h->heads)
+        return fail(Q3VL_ERR_INVALID_ARGUMENT, "bad checkpoint dimensions");
+    if (h->text_bits != 8 && h->text_bits != 16 && h->text_bits != 32)
+        return fail(Q3VL_ERR_UNSUPPORTED, "text_bits %d not read (8, 16 or 32)", h->text_bits);
+    if (h->text_bits == 8 && h->group_size <= 0)
+        return fail(Q3VL_ERR_INVALID_ARGUMENT, "group_size %d", h->group_size);
+    const size_t L = h->layers, H = h->hidden, I = h->intermediate, V = h->vocab;
+    const size_t hd = H / h->heads, QD = (size_t)h->heads * hd, KV = (size_t)h->kv_heads * hd;
+    size_t off = kCkHeaderBytes;
+    int rc = Q3VL_OK;
+    auto put = [&](int idx, size_t count, size_t rowlen, bool norm) {
+        q3vl_checkpoint_span t{};
+        t.bits = h->text_bits;
+        t.data_count = count;
+        if (h->text_bits == 8) {
+            const size_t grp = (h->group_quantized || norm) ? (size_t)h->group_size : rowlen;
+            if (count % grp) {
+                rc = fail(Q3VL_ERR_INVALID_ARGUMENT, "tensor %d: %zu values, not whole groups of %zu",
+                          idx, count, grp);
+                return;
+            }
+            t.group = (int)grp;
+            t.scales_offset = off;
+            t.scales_count = count / grp;
+            off += t.scales_count * 4;
+            t.data_offset = off;
+            off += count;
+        } else {
+            t.data_offset = off;
+            off += count * (size_t)(h->text_bits / 8);
+        }
+        sp[idx] = t;
+    };
+    put(Q3VL_CK_EMBED, V * H, H, false);
+    put(Q3VL_CK_ATTN_NORM, L * H, H, true);
+    put(Q3VL_CK_DOWN, L * H * I, I, false);
+    put(Q3VL_CK_GATE, L * I * H, H, false);
+    put(Q3VL_CK_UP, L * I * H, H, false);
+    put(Q3VL_CK_MLP_NORM, L * H, H, true);
+    put(Q3VL_CK_K_NORM, L * hd, hd, true);
+    put(Q3VL_CK_K, L * KV * H, H, false);
+    put(Q3VL_CK_O, L * H * H, H, false);  // {L, H, H} as load_model.cpp:186
+    put(Q3VL_CK_Q_NORM, L * hd, hd, true);
+    put(Q3VL_CK_Q, L * QD * H, H, false);
+    put(Q3VL_CK_V, L * KV * H, H, false);
+    put(Q3VL_CK_FINAL_NORM, H, H, true);
+    return rc;
+}
+
+}  // namespace
+
+extern "C" {
+
+int q3vl_checkpoint_read_header(const char *path, q3vl_checkpoint_header *hdr) {
+    if (!path || !hdr) return fail(Q3VL_ERR_INVALID_ARGUMENT, "null path / header");
+    FILE *f = fopen(path, "rb");
+    if (!f) return fail(Q3VL_ERR_INVALID_ARGUMENT, "cannot open %s", path);
+    unsigned char buf[kCkHeaderBytes];
+    const size_t got = fread(buf, 1, sizeof buf, f);
+    fclose(f);
+    if (got != sizeof buf) return fail(Q3VL_ERR_INVALID_ARGUMENT, "%s: shorter than the header", path);
+    memcpy(hdr, buf, sizeof buf);
+    return Q3VL_OK;
+}
+
+int q3vl_checkpoint_text_layout(const q3vl_checkpoint_header *hdr, q3vl_checkpoint_span *spans) {
+    return ck_layout(hdr, spans);
+}
+
+int q3vl_rope_tables(int rope_theta, int head_dim, int rows, float *cos_out, float *sin_out) {
+    if (!cos_out || !sin_out || head_dim <= 0 || head_dim % 2 || rows < 0)
+        return fail(Q3VL_ERR_INVALID_ARGUMENT, "bad RoPE table arguments");
+    const int half = head_dim / 2;
+    std::vector<float> inv_freq(half);
+    for (int i = 0; i < half; ++i)
+        inv_freq[i] = 1.0f / powf((float)rope_theta, (2.0f * i) / (float)head_dim);
+    for (int pos = 0; pos < rows; ++pos)
+        for (int i = 0; i < half; ++i) {
+            const float freq = pos * inv_freq[i];
+            cos_out[(size_t)pos * half + i] = cosf(freq);
+            sin_out[(size_t)pos * half + i] = sinf(freq);
+        }
+    return Q3VL_OK;
+}
+
+int q3vl_checkpoint_load(const char *path, int max_seq, q3vl_stream stream,
+                         q3vl_checkpoint **out) {
+    if (!out) return fail(Q3VL_ERR_INVALID_ARGUMENT, "null output");
+    *out = nullptr;
+    q3vl_checkpoint_header h;
+    int rc = q3vl_checkpoint_read_header(path, &h);
+    if (rc) return rc;
+    q3vl_checkpoint_span sp[Q3VL_CK_TEXT_TENSORS];
+    if ((rc = ck_layout(&h, sp))) return rc;
+    if (h.text_bits != 8)
+        return fail(Q3VL_ERR_UNSUPPORTED, "text_bits %d: the decode step runs int8 weights", h.text_bits);
+    if (!h.group_quantized)
+        return fail(Q3VL_ERR_UNSUPPORTED,
+                    "per-row scales (group_quantized = 0) are not served by the decode step");
+    if (max_seq <= 0) return fail(Q3VL_ERR_INVALID_ARGUMENT, "max_seq %d", max_seq);
+    const size_t end = sp[Q3VL_CK_FINAL_NORM].data_offset + sp[Q3VL_CK_FINAL_NORM].data_count;
+    {
+        q3vl_text_model dm{};
+        dm.vocab = h.vocab;
+        dm.hidden = h.hidden;
+        dm.intermediate = h.intermediate;
+        dm.layers = h.layers;
+        dm.heads = h.heads;
+        dm.kv_heads = h.kv_heads;
+        dm.head_dim = h.hidden / h.heads;
+        dm.max_seq = max_seq;
+        dm.group_size = h.group_size;
+        if ((rc = check_model_dims(&dm))) return rc;  // before any allocation
+    }
+
+    FILE *f = fopen(path, "rb");
+    if (!f) return fail(Q3VL_ERR_INVALID_ARGUMENT, "cannot open %s", path);
+    fseek(f, 0, SEEK_END);
+    const long fsize = ftell(f);
+    if (fsize < 0 || (size_t)fsize < end) {
+        fclose(f);
+        return fail(Q3VL_ERR_INVALID_ARGUMENT, "%s: %ld bytes, the text tensors end at %zu", path,
+                    fsize, end);
+    }
+
+    // device layout: every piece 256-byte aligned
+    const int hd = h.hidden / h.heads, half = hd / 2;
+    size_t off = 0;
+    size_t sc_at[Q3VL_CK_TEXT_TENSORS], da_at[Q3VL_CK_TEXT_TENSORS];
+    for (int i = 0; i < Q3VL_CK_TEXT_TENSORS; ++i) {
+        sc_at[i] = off;
+        off += align256(sp[i].scales_count * 4);
+        da_at[i] = off;
+        off += align256(sp[i].data_count);
+    }
+    const size_t rope_bytes = (size_t)max_seq * half * 4;
+    const size_t cos_at = off;
+    off += align256(rope_bytes);
+    const size_t sin_at = off;
+    off += align256(rope_bytes);
+
+    q3vl_checkpoint *ck = new q3vl_checkpoint{};
+    ck->hdr = h;
+    if (hipGetDevice(&ck->device) != hipSuccess || hipMalloc(&ck->dev, off) != hipSuccess) {
+        fclose(f);
+        delete ck;
+        return fail(Q3VL_ERR_OUT_OF_MEMORY, "checkpoint hipMalloc(%zu) failed", off);
+    }
+    auto undo = [&](int code) {
+        fclose(f);
+        (void)hipFree(ck->dev);
+        delete ck;
+        return code;
+    };
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    unsigned char *d = static_cast<unsigned char *>(ck->dev);
+    // Copies go through two pinned staging buffers in turn: the file read
+    // into one overlaps the host-to-device copy out of the other.
+    const size_t stage_bytes = (size_t)64 << 20;
+    void *stage[2] = {nullptr, nullptr};
+    hipEvent_t done[2] = {nullptr, nullptr};
+    bool used[2] = {false, false};
+    int k = 0;
+    for (int j = 0; j < 2 && !rc; ++j)
+        if (hipHostMalloc(&stage[j], stage_bytes, hipHostMallocDefault) != hipSuccess ||
+            hipEventCreateWithFlags(&done[j], hipEventDisableTiming) != hipSuccess)
+            rc = fail(Q3VL_ERR_OUT_OF_MEMORY, "pinned staging buffers");
+    auto copy_in = [&](size_t file_off, size_t bytes, size_t dev_off) -> int {
+        if (bytes && fseek(f, (long)file_off, SEEK_SET))
+            return fail(Q3VL_ERR_INVALID_ARGUMENT, "%s: seek failed at %zu", path, file_off);
+        while (bytes) {
+            const size_t n = bytes < stage_bytes ? bytes : stage_bytes;
+            if (used[k]) Q3VL_HIP(hipEventSynchronize(done[k]), "hipEventSynchronize");
+            if (fread(stage[k], 1, n, f) != n)
+                return fail(Q3VL_ERR_INVALID_ARGUMENT, "%s: read failed at %zu", path, file_off);
+            Q3VL_HIP(hipMemcpyAsync(d + dev_off, stage[k], n, hipMemcpyHostToDevice, st),
+                     "hipMemcpyAsync");
+            Q3VL_HIP(hipEventRecord(done[k], st), "hipEventRecord");
+            used[k] = true;
+            k ^= 1;
+            file_off += n;
+            dev_off += n;
+            bytes -= n;
+        }
+        return Q3VL_OK;
+    };
+    for (int i = 0; i < Q3VL_CK_TEXT_TENSORS && !rc; ++i) {
+        rc = copy_in(sp[i].scales_offset, sp[i].scales_count * 4, sc_at[i]);
+        if (!rc) rc = copy_in(sp[i].data_offset, sp[i].data_count, da_at[i]);
+    }
+    if (hipStreamSynchronize(st) != hipSuccess && !rc) rc = fail(Q3VL_ERR_HIP, "stream sync after the weight copies");
+    for (int j = 0; j < 2; ++j) {
+        if (done[j]) (void)hipEventDestroy(done[j]);
+        if (stage[j]) (void)hipHostFree(stage[j]);
+    }
+    if (!rc) {
+        std::vector<float> cs((size_t)max_seq * half), sn((size_t)max_seq * half);
+        rc = q3vl_rope_tables(h.rope_theta, hd, max_seq, cs.data(), sn.data());
+        if (!rc) {
+            hipError_t e = hipMemcpyAsync(d + cos_at, cs.data(), rope_bytes, hipMemcpyHostToDevice, st);
+            if (e == hipSuccess) e = hipMemcpyAsync(d + sin_at, sn.data(), rope_bytes, hipMemcpyHostToDevice, st);
+            if (e == hipSuccess) e = hipStreamSynchronize(st);
+            if (e != hipSuccess) rc = hip_fail(e, "RoPE table copy");
+        }
+    }
+    if (rc) return undo(rc);
+    fclose(f);
+
+    q3vl_text_model &m = ck->model;
+    m.vocab = h.vocab;
+    m.hidden = h.hidden;
+    m.intermediate = h.intermediate;
+    m.layers = h.layers;
+    m.heads = h.heads;
+    m.kv_heads = h.kv_heads;
+    m.head_dim = hd;
+    m.max_seq = max_seq;
+    m.group_size = h.group_size;
+    m.rms_eps = h.rms_eps;
+    auto W = [&](int i) { return reinterpret_cast<const int8_t *>(d + da_at[i]); };
+    auto S = [&](int i) { return reinterpret_cast<const float *>(d + sc_at[i]); };
+    m.embed_w = W(Q3VL_CK_EMBED);           m.embed_s = S(Q3VL_CK_EMBED);
+    m.final_norm_w = W(Q3VL_CK_FINAL_NORM); m.final_norm_s = S(Q3VL_CK_FINAL_NORM);
+    m.attn_norm_w = W(Q3VL_CK_ATTN_NORM);   m.attn_norm_s = S(Q3VL_CK_ATTN_NORM);
+    m.mlp_norm_w = W(Q3VL_CK_MLP_NORM);     m.mlp_norm_s = S(Q3VL_CK_MLP_NORM);
+    m.q_norm_w = W(Q3VL_CK_Q_NORM);         m.q_norm_s = S(Q3VL_CK_Q_NORM);
+    m.k_norm_w = W(Q3VL_CK_K_NORM);         m.k_norm_s = S(Q3VL_CK_K_NORM);
+    m.wq = W(Q3VL_CK_Q); m.sq = S(Q3VL_CK_Q);
+    m.wk = W(Q3VL_CK_K); m.sk = S(Q3VL_CK_K);
+    m.wv = W(Q3VL_CK_V); m.sv = S(Q3VL_CK_V);
+    m.wo = W(Q3VL_CK_O); m.so = S(Q3VL_CK_O);
+    m.wg = W(Q3VL_CK_GATE); m.sg = S(Q3VL_CK_GATE);
+    m.wu = W(Q3VL_CK_UP);   m.su = S(Q3VL_CK_UP);
+    m.wd = W(Q3VL_CK_DOWN); m.sd = S(Q3VL_CK_DOWN);
+    m.rope_cos = reinterpret_cast<const float *>(d + cos_at);
+    m.rope_sin = reinterpret_cast<const float *>(d + sin_at);
+    if ((rc = check_model(&m))) {
+        (void)hipFree(ck->dev);
+        delete ck;
+        return rc;
+    }
+    *out = ck;
+    return Q3VL_OK;
+}
+
+const q3vl_text_model *q3vl_checkpoint_text_model(const q3vl_checkpoint *ck) {
+    return ck ? &ck->model : nullptr;
+}
+
+int q3vl_checkpoint_header_of(const q3vl_checkpoint *ck, q3vl_checkpoint_header *hdr) {
+    if (!ck || !hdr) return fail(Q3VL_ERR_INVALID_ARGUMENT, "null checkpoint / header");
+    *hdr = ck->hdr;
+    return Q3VL_OK;
+}
+
+void q3vl_checkpoint_free(q3vl_checkpoint *ck) {
+    if (!ck) return;
+    int cur = 0;
+    const bool switched = hipGetDevice(&cur) == hipSuccess && cur != ck->device &&
+                          hipSetDevice(ck->device) == hipSuccess;
+    (void)hipDeviceSynchronize();
+    (void)hipFree(ck->dev);
+    if (switched) (void)hipSetDevice(cur);
+    delete ck;
+}
+
+int q3vl_quantize_groupwise(const float *x, size_t count, size_t group, int8_t *q, float *scales,
+                            q3vl_stream stream) {
+    if (!x || !q || !scales) return fail(Q3VL_ERR_INVALID_ARGUMENT, "null pointer");
+    if (!group || count % group)
+        return fail(Q3VL_ERR_INVALID_ARGUMENT, "count %zu is not a multiple of group %zu", count, group);
+    if (group > (size_t)INT32_MAX) return fail(Q3VL_ERR_UNSUPPORTED, "group %zu too large", group);
+    Q3VL_HIP(launch_quantize_export(x, count, group, q, scales, reinterpret_cast<hipStream_t>(stream)),
+             "quantize_export");
     return Q3VL_OK;
 }
 

@@ -49,6 +49,7 @@ Q3VL_INLINE uint32_t quant_pair(float lo, float hi) {
 // (53 >= 2*24+2), so the result equals the IEEE fp32 operation.
 Q3VL_INLINE float sqrt_rn(float x) { return (float)__builtin_sqrt((double)x); }
 Q3VL_INLINE float rcp_rn(float x) { return (float)(1.0 / (double)x); }
+Q3VL_INLINE float div_rn(float a, float b) { return (float)((double)a / (double)b); }
 
 // expf as the reference's host libm computes it (glibc >= 2.27 uses the
 // ARM optimized-routines expf by Szabolcs Nagy; on x86-64 CPUs with FMA the

@@ -14,6 +14,10 @@ hipError_t launch_quantize_i16(const float *A, int16_t *q, float *a_s, int M, in
 // transposed as a_sT[g * lda_s + m] for the GEMM epilogue.
 hipError_t launch_quantize_f16(const float *A, _Float16 *q, float *a_sT, int M, int K,
                                int gs, int ldq, int lda_s, hipStream_t st);
+// The exporter's weight quantizer: int8 values and one fp32 scale per group
+// of `group` consecutive values.
+hipError_t launch_quantize_export(const float *x, size_t count, size_t group, int8_t *q,
+                                  float *scales, hipStream_t st);
 
 // ------------------------------------------------------------ GEMV (M <= 8)
 // Up to three weight matrices stacked along N share one quantized activation.

@@ -76,4 +76,172 @@ hipError_t launch_quantize_f16(const float *A, _Float16 *q, float *a_sT, int M, 
     return launch_quant<_Float16>(A, q, a_sT, M, K, gs, ldq, 1, lda_s, st);
 }
 
+// ------------------------------------------------ exporter weight quantizer
+// quantize_groupwise (export_bin/export_qwen_bin.py:260-275) in numpy's fp32
+// arithmetic: m = max|x| + 1e-8, s = m / 127, q = round half to even of
+// x / s, clipped to [-127, 127] (|x / s| <= 127 (1 + 2^-24) for finite x, so
+// no value is clipped and the int8 cast is exact). The values are finite, as
+// the exporter's are.
+//
+// s is the IEEE fp32 quotient (div_rn). x / s is computed per element from
+// r = RN(1/s) with two residual corrections (div_q below), which gives the
+// IEEE quotient whenever it is >= 2^-80 in magnitude: the first correction
+// makes the estimate faithful, the second is then correctly rounded
+// (Markstein's theorem: r correctly rounded, faithful estimate, exact
+// fma residual). Below 2^-80 the residual may underflow, and both quotients
+// round to the integer 0, so q is always the exporter's.
+Q3VL_INLINE float div_q(float x, float s, float r) {
+    const float y0 = x * r;
+    const float y1 = fmaf(fmaf(-s, y0, x), r, y0);
+    return fmaf(fmaf(-s, y1, x), r, y1);
+}
+
+typedef float fx4 __attribute__((ext_vector_type(4)));
+
+Q3VL_INLINE uint32_t quant4(fx4 v, float s, float r) {
+    auto one = [&](float x) {
+        const float t = fminf(fmaxf(__builtin_rintf(div_q(x, s, r)), -127.0f), 127.0f);
+        return (uint32_t)(uint8_t)(int8_t)t;
+    };
+    return one(v.x) | (one(v.y) << 8) | (one(v.z) << 16) | (one(v.w) << 24);
+}
+
+Q3VL_INLINE float absmax4(fx4 v) {
+    return fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+}
+
+// Groups of G <= 256 values (a power of two >= 4): G/4 lanes share a group,
+// one float4 per lane, so a wave covers 256 consecutive values (a "chunk")
+// per pass and U chunks are in flight per loop iteration.
+template <int G, int U>
+__global__ __launch_bounds__(256) void quantize_export_vec_kernel(const fx4 *__restrict__ x,
+                                                                  size_t n4,
+                                                                  uint32_t *__restrict__ q,
+                                                                  float *__restrict__ scales) {
+    constexpr int L = G / 4;
+    const int lane = threadIdx.x & 63;
+    const size_t wave = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const size_t nwaves = ((size_t)gridDim.x * blockDim.x) >> 6;
+    for (size_t c0 = wave * U; c0 * 64 < n4; c0 += nwaves * U) {
+        fx4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const size_t i = (c0 + u) * 64 + lane;
+            v[u] = i < n4 ? __builtin_nontemporal_load(x + i) : fx4{0.f, 0.f, 0.f, 0.f};
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const size_t i = (c0 + u) * 64 + lane;
+            float m = absmax4(v[u]);
+#pragma unroll
+            for (int off = L / 2; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+            const float s = div_rn(m + 1e-8f, 127.0f);
+            const float r = rcp_rn(s);
+            if (i < n4) {  // n4 is a multiple of L: a group is wholly in or out
+                if ((lane & (L - 1)) == 0) scales[i / L] = s;
+                q[i] = quant4(v[u], s, r);
+            }
+        }
+    }
+}
+
+// Groups of G > 256 values, G a multiple of 4: one wave per group; the max
+// pass and the quantize pass each stream the group's float4s (the second
+// read is an L2 hit for groups up to a few KB).
+__global__ __launch_bounds__(256) void quantize_export_wave_kernel(const fx4 *__restrict__ x,
+                                                                   size_t ngroups, int G4,
+                                                                   uint32_t *__restrict__ q,
+                                                                   float *__restrict__ scales) {
+    const int lane = threadIdx.x & 63;
+    const size_t wave = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const size_t nwaves = ((size_t)gridDim.x * blockDim.x) >> 6;
+    for (size_t g = wave; g < ngroups; g += nwaves) {
+        const fx4 *xg = x + g * (size_t)G4;
+        float m0 = 0.0f, m1 = 0.0f;
+        int i = lane;
+        for (; i + 64 < G4; i += 128) {
+            m0 = fmaxf(m0, absmax4(xg[i]));
+            m1 = fmaxf(m1, absmax4(xg[i + 64]));
+        }
+        if (i < G4) m0 = fmaxf(m0, absmax4(xg[i]));
+        float m = fmaxf(m0, m1);
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+        const float s = div_rn(m + 1e-8f, 127.0f);
+        const float r = rcp_rn(s);
+        if (lane == 0) scales[g] = s;
+        uint32_t *qg = q + g * (size_t)G4;
+        for (int j = lane; j < G4; j += 64) qg[j] = quant4(xg[j], s, r);
+    }
+}
+
+// Any other group size or alignment: W lanes (a power of two, W <= group,
+// W <= 64) share a group, one value per lane per step.
+__global__ __launch_bounds__(256) void quantize_export_kernel(const float *__restrict__ x,
+                                                              size_t ngroups, int group, int W,
+                                                              int8_t *__restrict__ q,
+                                                              float *__restrict__ scales) {
+    const int lane = threadIdx.x & 63;
+    const int sub = lane & (W - 1);
+    const int per_wave = 64 / W;
+    const size_t wave = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const size_t nwaves = ((size_t)gridDim.x * blockDim.x) >> 6;
+    for (size_t g0 = wave * per_wave; g0 < ngroups; g0 += nwaves * per_wave) {
+        const size_t gi = g0 + lane / W;
+        const bool active = gi < ngroups;
+        const float *xg = x + (active ? gi : 0) * (size_t)group;
+        float m = 0.0f;
+        if (active)
+            for (int i = sub; i < group; i += W) m = fmaxf(m, fabsf(xg[i]));
+        for (int off = W >> 1; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+        const float s = div_rn(m + 1e-8f, 127.0f);
+        const float r = rcp_rn(s);
+        if (!active) continue;
+        if (sub == 0) scales[gi] = s;
+        int8_t *qg = q + gi * (size_t)group;
+        for (int i = sub; i < group; i += W)
+            qg[i] = (int8_t)fminf(fmaxf(__builtin_rintf(div_q(xg[i], s, r)), -127.0f), 127.0f);
+    }
+}
+
+static unsigned grid_for(size_t waves) {
+    const size_t blocks = (waves + 3) / 4;  // 4 waves per block
+    return (unsigned)(blocks < (1u << 20) ? blocks : (1u << 20));
+}
+
+hipError_t launch_quantize_export(const float *x, size_t count, size_t group, int8_t *q,
+                                  float *scales, hipStream_t st) {
+    if (group == 0 || count % group != 0 || group > (size_t)INT32_MAX) return hipErrorInvalidValue;
+    const size_t ngroups = count / group;
+    if (ngroups == 0) return hipSuccess;
+    const bool vec = group % 4 == 0 && ((uintptr_t)x & 15u) == 0 && ((uintptr_t)q & 3u) == 0;
+    if (vec && group <= 256 && (group & (group - 1)) == 0) {
+        constexpr int U = 2;
+        const size_t n4 = count / 4;
+        const size_t waves = ((n4 + 63) / 64 + U - 1) / U;
+        const fx4 *x4 = reinterpret_cast<const fx4 *>(x);
+        uint32_t *q4 = reinterpret_cast<uint32_t *>(q);
+        switch (group) {
+#define Q3VL_XCASE(G)                                                                       \
+    case G:                                                                                 \
+        quantize_export_vec_kernel<G, U><<<grid_for(waves), 256, 0, st>>>(x4, n4, q4, scales); \
+        return hipGetLastError();
+            Q3VL_XCASE(4) Q3VL_XCASE(8) Q3VL_XCASE(16) Q3VL_XCASE(32) Q3VL_XCASE(64)
+            Q3VL_XCASE(128) Q3VL_XCASE(256)
+#undef Q3VL_XCASE
+        }
+    }
+    if (vec && group > 256) {
+        quantize_export_wave_kernel<<<grid_for(ngroups), 256, 0, st>>>(
+            reinterpret_cast<const fx4 *>(x), ngroups, (int)(group / 4),
+            reinterpret_cast<uint32_t *>(q), scales);
+        return hipGetLastError();
+    }
+    int W = 64;
+    while ((size_t)W > group) W >>= 1;
+    const size_t waves = (ngroups + (64 / W) - 1) / (64 / W);
+    quantize_export_kernel<<<grid_for(waves), 256, 0, st>>>(x, ngroups, (int)group, W, q, scales);
+    return hipGetLastError();
+}
+
 }  // namespace q3vl

@@ -57,6 +57,7 @@ def _declare(lib):
         "q3vl_weight_lookup": (i, [_vp, _vp, _vp]),
         "q3vl_weight_release": (i, [_vp]),
         "q3vl_weight_release_all": (i, []),
+        "q3vl_quantize_groupwise": (i, [_vp, _sz, _sz, _vp, _vp, _vp]),
     }
     for name, (res, args) in sigs.items():
         fn = getattr(lib, name)
@@ -245,3 +246,24 @@ def swiglu(gate, up, stream=None):
     _need(up, torch.float32, "up")
     _check(lib().q3vl_swiglu(_ptr(gate), _ptr(up), gate.numel(), _stream(stream)))
     return gate
+
+
+def quantize_groupwise(x, group, q=None, scales=None, stream=None):
+    """The checkpoint exporter's weight quantizer on the device
+    (export_bin/export_qwen_bin.py:260-275): x fp32 (any shape, numel a
+    multiple of group) -> (q int8 like x, scales fp32 [numel/group])."""
+    torch = _torch()
+    _need(x, torch.float32, "x")
+    n = x.numel()
+    if group <= 0 or n % group:
+        raise ValueError(f"{n} values are not whole groups of {group}")
+    q = torch.empty(x.shape, dtype=torch.int8, device=x.device) if q is None else q
+    scales = (torch.empty((n // group,), dtype=torch.float32, device=x.device)
+              if scales is None else scales)
+    _need(q, torch.int8, "q")
+    _need(scales, torch.float32, "scales")
+    if q.numel() != n or scales.numel() != n // group:
+        raise ValueError("q / scales sizes do not match x")
+    _check(lib().q3vl_quantize_groupwise(_ptr(x), n, group, _ptr(q), _ptr(scales),
+                                         _stream(stream)))
+    return q, scales

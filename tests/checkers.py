@@ -83,6 +83,16 @@ class Oracle:
         return g
 
     # ---- decode step
+    def quantize_groupwise(self, x, group):
+        """The exporter's group quantizer: (q int8 like x, scales [x.size/group])."""
+        L = self.lib
+        L.orc_quantize_groupwise.argtypes = [_vp, _sz, _sz, _vp, _vp]
+        x = np.ascontiguousarray(x, np.float32)
+        q = np.zeros(x.shape, np.int8)
+        s = np.zeros(x.size // group, np.float32)
+        L.orc_quantize_groupwise(_p(x), x.size, group, _p(q), _p(s))
+        return q, s
+
     def decode_step(self, dims, arrays, k_cache, v_cache, token, pos, kv_fp16=True):
         """Returns (next_id, logits); updates the caches at pos in place."""
         L = self.lib
@@ -157,6 +167,11 @@ def _model_struct(dims, arrays):
     return st
 
 
+class _RefCkTensor(ctypes.Structure):
+    _fields_ = [("data", _vp), ("scales", _vp), ("count", _sz), ("group", _sz),
+                ("dtype", ctypes.c_int)]
+
+
 class Reference:
     def __init__(self, lib):
         self.lib = lib
@@ -185,6 +200,35 @@ class Reference:
         u = np.ascontiguousarray(up, np.float32)
         self.lib.ref_swiglu(_p(g), _p(u), g.size)
         return g
+
+    def checkpoint_open(self, path):
+        """The reference loader over a checkpoint file: (header fields in file
+        order with rms_eps as a float, [tensor dicts] for the 13 text then 27
+        vision groups, close())."""
+        L = self.lib
+        L.ref_checkpoint_open.restype = _vp
+        L.ref_checkpoint_open.argtypes = [ctypes.c_char_p, _vp, _vp]
+        L.ref_checkpoint_close.argtypes = [_vp]
+        cfg = np.zeros(25, np.int32)
+        ts = (_RefCkTensor * 40)()
+        h = L.ref_checkpoint_open(path.encode(), _p(cfg), ts)
+        if not h:
+            raise RuntimeError(f"reference loader mapped nothing from {path}")
+        fields = [int(v) for v in cfg]
+        fields[8] = float(cfg[8:9].view(np.float32)[0])
+        out = [dict(data=t.data, scales=t.scales, count=t.count, group=t.group, dtype=t.dtype)
+               for t in ts]
+        return fields, out, (lambda: L.ref_checkpoint_close(h))
+
+    def rope_precompute(self, rope_theta, hidden, heads, seq_len):
+        """qwen_rope_precompute's (cos, sin) [3, seq_len, head_dim/2]."""
+        L = self.lib
+        L.ref_rope_precompute.argtypes = [ctypes.c_int] * 4 + [_vp, _vp]
+        half = hidden // heads // 2
+        cos = np.zeros((3, seq_len, half), np.float32)
+        sin = np.zeros((3, seq_len, half), np.float32)
+        L.ref_rope_precompute(rope_theta, hidden, heads, seq_len, _p(cos), _p(sin))
+        return cos, sin
 
     def rms_norm_i8(self, x, w, ws, gs, eps):
         L = self.lib
