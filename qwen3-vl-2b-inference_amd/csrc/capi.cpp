@@ -10,8 +10,12 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <atomic>
+#include <fcntl.h>
 #include <mutex>
 #include <string>
+#include <thread>
+#include <unistd.h>
 #include <unordered_map>
 #include <vector>
 
@@ -658,6 +662,94 @@ static_assert(sizeof(q3vl_checkpoint_header) == kCkHeaderBytes,
 
 // map_tensor's walk over the text groups (load_model.cpp:146-195): per group,
 // the scales (int8) then the values; norm tensors always group-quantized.
+// One byte range of a checkpoint file and where it goes in device memory.
+struct FilePiece {
+    size_t file_off, bytes, dev_off;
+};
+
+// Copies file byte ranges to device memory on the current device. kReaders
+// threads each take 16 MB jobs in turn, read them with pread into one of
+// their own two pinned buffers and copy them on their own stream, so the
+// file reads (memcpy-bound from the page cache) run in parallel and overlap
+// the host-to-device copies. Synchronous: every copy has landed on return.
+int copy_file_to_device(int fd, const char *path, const std::vector<FilePiece> &pieces,
+                        unsigned char *d) {
+    constexpr int kReaders = 4;
+    constexpr size_t kJob = (size_t)16 << 20;
+    std::vector<FilePiece> jobs;
+    for (const FilePiece &p : pieces)
+        for (size_t o = 0; o < p.bytes; o += kJob)
+            jobs.push_back({p.file_off + o, p.bytes - o < kJob ? p.bytes - o : kJob, p.dev_off + o});
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess) return fail(Q3VL_ERR_HIP, "hipGetDevice failed");
+    std::atomic<size_t> next{0};
+    std::atomic<bool> stop{false};
+    std::mutex mu;
+    int err_code = Q3VL_OK;
+    std::string err_msg;
+    auto set_err = [&](int code, std::string msg) {
+        std::lock_guard<std::mutex> lk(mu);
+        if (err_code == Q3VL_OK) {
+            err_code = code;
+            err_msg = std::move(msg);
+        }
+        stop = true;
+    };
+    auto worker = [&]() {
+        if (hipSetDevice(device) != hipSuccess) return set_err(Q3VL_ERR_HIP, "hipSetDevice failed");
+        hipStream_t st = nullptr;
+        void *stage[2] = {nullptr, nullptr};
+        hipEvent_t done[2] = {nullptr, nullptr};
+        bool used[2] = {false, false};
+        bool ok = hipStreamCreateWithFlags(&st, hipStreamNonBlocking) == hipSuccess;
+        for (int j = 0; j < 2 && ok; ++j)
+            ok = hipHostMalloc(&stage[j], kJob, hipHostMallocDefault) == hipSuccess &&
+                 hipEventCreateWithFlags(&done[j], hipEventDisableTiming) == hipSuccess;
+        if (!ok) set_err(Q3VL_ERR_OUT_OF_MEMORY, "pinned staging buffers / reader stream");
+        for (int k = 0; ok && !stop; k ^= 1) {
+            const size_t j = next++;
+            if (j >= jobs.size()) break;
+            const FilePiece &jb = jobs[j];
+            if (used[k] && hipEventSynchronize(done[k]) != hipSuccess) {
+                set_err(Q3VL_ERR_HIP, "hipEventSynchronize failed");
+                break;
+            }
+            size_t got = 0;
+            while (got < jb.bytes) {
+                const ssize_t n = pread(fd, static_cast<char *>(stage[k]) + got, jb.bytes - got,
+                                        (off_t)(jb.file_off + got));
+                if (n <= 0) break;
+                got += (size_t)n;
+            }
+            if (got != jb.bytes) {
+                char buf[256];
+                snprintf(buf, sizeof buf, "%s: read failed at %zu", path, jb.file_off + got);
+                set_err(Q3VL_ERR_INVALID_ARGUMENT, buf);
+                break;
+            }
+            hipError_t e = hipMemcpyAsync(d + jb.dev_off, stage[k], jb.bytes, hipMemcpyHostToDevice, st);
+            if (e == hipSuccess) e = hipEventRecord(done[k], st);
+            if (e != hipSuccess) {
+                set_err(Q3VL_ERR_HIP, std::string("checkpoint copy: ") + hipGetErrorString(e));
+                break;
+            }
+            used[k] = true;
+        }
+        if (st && hipStreamSynchronize(st) != hipSuccess) set_err(Q3VL_ERR_HIP, "reader stream sync failed");
+        for (int j = 0; j < 2; ++j) {
+            if (done[j]) (void)hipEventDestroy(done[j]);
+            if (stage[j]) (void)hipHostFree(stage[j]);
+        }
+        if (st) (void)hipStreamDestroy(st);
+    };
+    const int nthreads = (int)(jobs.size() < (size_t)kReaders ? jobs.size() : (size_t)kReaders);
+    std::vector<std::thread> pool;
+    for (int t = 0; t < nthreads; ++t) pool.emplace_back(worker);
+    for (std::thread &t : pool) t.join();
+    if (err_code != Q3VL_OK) return fail(err_code, "%s", err_msg.c_str());
+    return Q3VL_OK;
+}
+
 int ck_layout(const q3vl_checkpoint_header *h, q3vl_checkpoint_span *sp) {
     if (!h || !sp) return fail(Q3VL_ERR_INVALID_ARGUMENT, "null header / spans");
     if (h->vocab <= 0 || h->hidden <= 0 || h->intermediate <= 0 || h->layers <= 0 ||
@@ -776,24 +868,26 @@ int q3vl_checkpoint_load(const char *path, int max_seq, q3vl_stream stream,
         if ((rc = check_model_dims(&dm))) return rc;  // before any allocation
     }
 
-    FILE *f = fopen(path, "rb");
-    if (!f) return fail(Q3VL_ERR_INVALID_ARGUMENT, "cannot open %s", path);
-    fseek(f, 0, SEEK_END);
-    const long fsize = ftell(f);
+    const int fd = open(path, O_RDONLY | O_CLOEXEC);
+    if (fd < 0) return fail(Q3VL_ERR_INVALID_ARGUMENT, "cannot open %s", path);
+    const off_t fsize = lseek(fd, 0, SEEK_END);
     if (fsize < 0 || (size_t)fsize < end) {
-        fclose(f);
-        return fail(Q3VL_ERR_INVALID_ARGUMENT, "%s: %ld bytes, the text tensors end at %zu", path,
-                    fsize, end);
+        close(fd);
+        return fail(Q3VL_ERR_INVALID_ARGUMENT, "%s: %lld bytes, the text tensors end at %zu", path,
+                    (long long)fsize, end);
     }
 
     // device layout: every piece 256-byte aligned
     const int hd = h.hidden / h.heads, half = hd / 2;
     size_t off = 0;
+    std::vector<FilePiece> pieces;
     size_t sc_at[Q3VL_CK_TEXT_TENSORS], da_at[Q3VL_CK_TEXT_TENSORS];
     for (int i = 0; i < Q3VL_CK_TEXT_TENSORS; ++i) {
         sc_at[i] = off;
+        pieces.push_back({sp[i].scales_offset, sp[i].scales_count * 4, off});
         off += align256(sp[i].scales_count * 4);
         da_at[i] = off;
+        pieces.push_back({sp[i].data_offset, sp[i].data_count, off});
         off += align256(sp[i].data_count);
     }
     const size_t rope_bytes = (size_t)max_seq * half * 4;
@@ -805,58 +899,15 @@ int q3vl_checkpoint_load(const char *path, int max_seq, q3vl_stream stream,
     q3vl_checkpoint *ck = new q3vl_checkpoint{};
     ck->hdr = h;
     if (hipGetDevice(&ck->device) != hipSuccess || hipMalloc(&ck->dev, off) != hipSuccess) {
-        fclose(f);
+        close(fd);
         delete ck;
         return fail(Q3VL_ERR_OUT_OF_MEMORY, "checkpoint hipMalloc(%zu) failed", off);
     }
-    auto undo = [&](int code) {
-        fclose(f);
-        (void)hipFree(ck->dev);
-        delete ck;
-        return code;
-    };
-    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     unsigned char *d = static_cast<unsigned char *>(ck->dev);
-    // Copies go through two pinned staging buffers in turn: the file read
-    // into one overlaps the host-to-device copy out of the other.
-    const size_t stage_bytes = (size_t)64 << 20;
-    void *stage[2] = {nullptr, nullptr};
-    hipEvent_t done[2] = {nullptr, nullptr};
-    bool used[2] = {false, false};
-    int k = 0;
-    for (int j = 0; j < 2 && !rc; ++j)
-        if (hipHostMalloc(&stage[j], stage_bytes, hipHostMallocDefault) != hipSuccess ||
-            hipEventCreateWithFlags(&done[j], hipEventDisableTiming) != hipSuccess)
-            rc = fail(Q3VL_ERR_OUT_OF_MEMORY, "pinned staging buffers");
-    auto copy_in = [&](size_t file_off, size_t bytes, size_t dev_off) -> int {
-        if (bytes && fseek(f, (long)file_off, SEEK_SET))
-            return fail(Q3VL_ERR_INVALID_ARGUMENT, "%s: seek failed at %zu", path, file_off);
-        while (bytes) {
-            const size_t n = bytes < stage_bytes ? bytes : stage_bytes;
-            if (used[k]) Q3VL_HIP(hipEventSynchronize(done[k]), "hipEventSynchronize");
-            if (fread(stage[k], 1, n, f) != n)
-                return fail(Q3VL_ERR_INVALID_ARGUMENT, "%s: read failed at %zu", path, file_off);
-            Q3VL_HIP(hipMemcpyAsync(d + dev_off, stage[k], n, hipMemcpyHostToDevice, st),
-                     "hipMemcpyAsync");
-            Q3VL_HIP(hipEventRecord(done[k], st), "hipEventRecord");
-            used[k] = true;
-            k ^= 1;
-            file_off += n;
-            dev_off += n;
-            bytes -= n;
-        }
-        return Q3VL_OK;
-    };
-    for (int i = 0; i < Q3VL_CK_TEXT_TENSORS && !rc; ++i) {
-        rc = copy_in(sp[i].scales_offset, sp[i].scales_count * 4, sc_at[i]);
-        if (!rc) rc = copy_in(sp[i].data_offset, sp[i].data_count, da_at[i]);
-    }
-    if (hipStreamSynchronize(st) != hipSuccess && !rc) rc = fail(Q3VL_ERR_HIP, "stream sync after the weight copies");
-    for (int j = 0; j < 2; ++j) {
-        if (done[j]) (void)hipEventDestroy(done[j]);
-        if (stage[j]) (void)hipHostFree(stage[j]);
-    }
+    rc = copy_file_to_device(fd, path, pieces, d);
+    close(fd);
     if (!rc) {
+        hipStream_t st = reinterpret_cast<hipStream_t>(stream);
         std::vector<float> cs((size_t)max_seq * half), sn((size_t)max_seq * half);
         rc = q3vl_rope_tables(h.rope_theta, hd, max_seq, cs.data(), sn.data());
         if (!rc) {
@@ -866,8 +917,11 @@ int q3vl_checkpoint_load(const char *path, int max_seq, q3vl_stream stream,
             if (e != hipSuccess) rc = hip_fail(e, "RoPE table copy");
         }
     }
-    if (rc) return undo(rc);
-    fclose(f);
+    if (rc) {
+        (void)hipFree(ck->dev);
+        delete ck;
+        return rc;
+    }
 
     q3vl_text_model &m = ck->model;
     m.vocab = h.vocab;
