@@ -442,23 +442,37 @@ __global__ __launch_bounds__(GEMV_MAX_THREADS) void gemv_kernel(GemvArgs a, int 
                 wp[2 * d + 1] = hi2(wd[d]);
             }
             int32_t *Gd = seg_G(row_seg(cur, r));
-            if constexpr (LANES) {
+            if constexpr (LANES && T <= 8) {
+                // the 8 lane sums of this thread's 16 bytes, then reduced
+                // over the group's T threads so that thread tg holds the
+                // group totals of lanes tg*W .. tg*W + W-1 and writes them
+                constexpr int W = 8 / T;
+                int32_t p[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) p[j] = dot2(qp[0][j], wp[j], 0);
+                scatter_sums<T>(p, tg);
+                if (act) {
+#pragma unroll
+                    for (int k = 0; k < W; ++k) accb[(r * 8 + tg * W + k) * ld + g] = p[k] >> 8;
+                }
+                if (Gd) {  // the group sum: this thread's lanes, then the run's
+                    int32_t tot = 0;
+#pragma unroll
+                    for (int k = 0; k < W; ++k) tot += p[k] >> 8;
+                    tot = run_sum<T>(tot);
+                    if (act && tg == 0) Gd[(size_t)row_n(cur, r) * Kg + g] = tot;
+                }
+            } else if constexpr (LANES) {
                 int32_t p[8];
 #pragma unroll
                 for (int j = 0; j < 8; ++j) p[j] = run_sum<T>(dot2(qp[0][j], wp[j], 0));
-                // every thread of the group holds all 8 sums: thread tg writes
-                // 8/T of them (one LDS write instruction per 8/T lanes sums
-                // instead of 8 by the group's first thread)
-                constexpr int WPT = T <= 8 ? 8 / T : 1;
-                if (act && (T <= 8 || tg < 8)) {
+                // every thread of the group holds all 8 sums: threads 0..7
+                // of the group write one each
+                if (act && tg < 8) {
+                    int32_t v = p[0];
 #pragma unroll
-                    for (int k = 0; k < WPT; ++k) {
-                        const int j = (T <= 8 ? tg * WPT : tg) + k;
-                        int32_t v = p[0];
-#pragma unroll
-                        for (int jj = 1; jj < 8; ++jj) v = jj == j ? p[jj] : v;
-                        accb[(r * 8 + j) * ld + g] = v >> 8;
-                    }
+                    for (int jj = 1; jj < 8; ++jj) v = jj == tg ? p[jj] : v;
+                    accb[(r * 8 + tg) * ld + g] = v >> 8;
                 }
                 if (act && tg == 0) {
                     if (Gd) {

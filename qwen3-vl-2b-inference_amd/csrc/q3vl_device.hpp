@@ -159,4 +159,47 @@ Q3VL_INLINE int32_t run_sum(int32_t v) {
     return v;
 }
 
+// Reduce-scatter of 8 per-thread sums over the aligned run of T threads
+// (T = 1, 2, 4 or 8) that holds one group: thread tg of the run ends with
+// the run's totals for sums j = tg*W .. tg*W + W-1 (W = 8/T) in v[0..W).
+// Each step halves the set by one bit of tg: the thread keeps the half its
+// final sums lie in and adds its partner's copy of that half (the partner
+// differs in that bit: half mirror for bit 2, xor 2 for bit 1, xor 1 for
+// bit 0). Integer adds, so the totals equal any other summation order.
+template <int T>
+Q3VL_INLINE void scatter_sums(int32_t (&v)[8], int tg) {
+    static_assert(T == 1 || T == 2 || T == 4 || T == 8, "group run of 1, 2, 4 or 8 threads");
+    // every index below is a compile-time constant (a select over a
+    // run-time index would become compare chains)
+    if constexpr (T == 8) {
+        const bool hi = (tg & 4) != 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int32_t keep = hi ? v[4 + k] : v[k];
+            const int32_t send = hi ? v[k] : v[4 + k];
+            v[k] = keep + dpp_half_mirror(send);
+        }
+    }
+    if constexpr (T >= 4) {
+        constexpr int H = T == 8 ? 2 : 4;
+        const bool hi = (tg & 2) != 0;
+#pragma unroll
+        for (int k = 0; k < H; ++k) {
+            const int32_t keep = hi ? v[H + k] : v[k];
+            const int32_t send = hi ? v[k] : v[H + k];
+            v[k] = keep + dpp_xor2(send);
+        }
+    }
+    if constexpr (T >= 2) {
+        constexpr int H = T == 8 ? 1 : T == 4 ? 2 : 4;
+        const bool hi = (tg & 1) != 0;
+#pragma unroll
+        for (int k = 0; k < H; ++k) {
+            const int32_t keep = hi ? v[H + k] : v[k];
+            const int32_t send = hi ? v[k] : v[H + k];
+            v[k] = keep + dpp_xor1(send);
+        }
+    }
+}
+
 }  // namespace q3vl
