@@ -87,6 +87,17 @@ __host__ __device__ constexpr int md_mode(int md) {
 }
 __host__ __device__ constexpr int md_nseg(int md) { return md == MD_SWIGLU ? 2 : 1; }
 
+// The fused norm's chain-major copy of the activation row: 8 rows (one per
+// lane chain of the sum of squares), row l holding x[l + 8t] at position t.
+// With SEG (row length 2048: 256 positions a chain), each row is cut into 8
+// segments of 32 positions with 4 floats of padding after each, so that the
+// 64 lanes of a wave, one segment each, read their segments without bank
+// conflicts. Words per row:
+__host__ __device__ constexpr bool norm_seg(int KC) { return KC == 2048; }
+__host__ __device__ constexpr int norm_row_words(int K, bool seg) {
+    return seg ? K / 8 + K / 64 + 4 : K / 8 + 4;
+}
+
 // KC: the row length K when it is fixed at compile time (the decode step's
 // 2048 and 6144), 0 for a run-time K. With KC set, every quantity derived
 // from K (group count, LDS layout, index divisions) is a constant.
@@ -164,7 +175,8 @@ __global__ __launch_bounds__(GEMV_MAX_THREADS) void gemv_kernel(GemvArgs a, int 
     // the chain-major copy of the row for a fused norm (8 rows of K/8 + 4),
     // and >= 2*nthr (argmax scratch)
     const bool has_norm = norm_w != nullptr;
-    const int nrs = K / 8 + 4;
+    constexpr bool SEGN = norm_seg(KC);
+    const int nrs = norm_row_words(K, SEGN);
     // The staged row keeps 4 floats of padding after every group, so the
     // threads of a wave, each reading its own group, hit distinct banks.
     const int xpad = 4 * (16 * nthr / GS);
@@ -244,7 +256,8 @@ __global__ __launch_bounds__(GEMV_MAX_THREADS) void gemv_kernel(GemvArgs a, int 
             // chain-major copy: element 4i + c sits in chain 4*(i&1) + c at i/2
             auto put4 = [&](int i, const float4 &v) {
                 if (i < K / 4) {
-                    float *d = xn + 4 * (i & 1) * nrs + (i >> 1);
+                    const int t = i >> 1;  // position in the chain
+                    float *d = xn + 4 * (i & 1) * nrs + (SEGN ? t + 4 * (t >> 5) : t);
                     d[0] = v.x;
                     d[nrs] = v.y;
                     d[2 * nrs] = v.z;
@@ -260,7 +273,39 @@ __global__ __launch_bounds__(GEMV_MAX_THREADS) void gemv_kernel(GemvArgs a, int 
         if (has_norm) {
             // sum of squares in the reference's 8-lane order (lanes 0..7 of
             // wave 0), then inv = 1/sqrt(ss/K + eps) in fp32
-            if (tid < 64) {
+            if (SEGN && tid < 64) {
+                // lane 8l + j holds segment j (positions 32j .. 32j+31) of
+                // chain l in registers. Segment s: every lane runs its 32
+                // FMAs, but only lanes j == s carry their chain (the others'
+                // sums are discarded); a row shift then hands each chain's
+                // sum to the lane of its next segment. So chain l is the
+                // reference's FMA sequence over t = 0..255, with no LDS read
+                // between its FMAs.
+                const float *sg = xn + (tid >> 3) * nrs + (tid & 7) * 36;
+                float4 X[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) X[u] = reinterpret_cast<const float4 *>(sg)[u];
+                float acc = 0.0f;
+#pragma unroll
+                for (int sgm = 0; sgm < 8; ++sgm) {
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) {
+                        acc = fmaf(X[u].x, X[u].x, acc);
+                        acc = fmaf(X[u].y, X[u].y, acc);
+                        acc = fmaf(X[u].z, X[u].z, acc);
+                        acc = fmaf(X[u].w, X[u].w, acc);
+                    }
+                    if (sgm < 7)  // row_shr:1 (lane i takes lane i-1 inside each row of 16)
+                        acc = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                                  0, __builtin_bit_cast(int, acc), 0x111, 0xF, 0xF, false));
+                }
+                // chain l's sum sits in lane 8l + 7; added in chain order
+                float ss = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, acc), 7));
+#pragma unroll
+                for (int l = 1; l < 8; ++l)
+                    ss = ss + __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, acc), 8 * l + 7));
+                if (tid == 0) s_norm_inv = rcp_rn(sqrt_rn(ss * rcp_rn((float)K) + a.norm_eps));
+            } else if (tid < 64) {
                 float acc = 0.0f;
                 if (tid < 8) {
                     const float *row = xn + tid * nrs;
@@ -728,7 +773,8 @@ static hipError_t launch_gemv_t(const GemvArgs &a, int *grid_out, hipStream_t st
     const int nthr = K / 16 > 64 ? K / 16 : 64;
     const int ld = group_ld(Kg);
     const int acc_words = (LANES ? 8 * R : MR * R) * ld;
-    const int stage_need = 16 * nthr + 4 * (16 * nthr / GS) + (a.norm_w ? 8 * (K / 8 + 4) : 0);
+    const int stage_need = 16 * nthr + 4 * (16 * nthr / GS) +
+                           (a.norm_w ? 8 * norm_row_words(K, norm_seg(KC)) : 0);
     const int stage_words = acc_words > stage_need ? acc_words : stage_need;
     const size_t lds = (size_t)(stage_words + MR * Kg + R * ld + MR * R) * 4;
 
