@@ -309,7 +309,7 @@ __global__ __launch_bounds__(256, 2) void gemm_i8_kernel(GemmArgs a) {
 // * Tile (32*MT*2) x (32*NT*2), 4 waves in 2x2, each wave (32*MT) x (32*NT);
 //   the host picks MT/NT so the grid fills the device. SWIGLU (NT = 2): the
 //   block's B rows 0..63 are gate rows, 64..127 the same up rows.
-template <int MT, int NT, bool SWIGLU, int D>
+template <int MT, int NT, bool SWIGLU, int D, bool PIPE>
 __global__ __launch_bounds__(256, 2) void gemm_g64_kernel(GemmArgs a) {
     constexpr int TBM = 64 * MT, TBN = 64 * NT;
     constexpr int ASTG = TBM * 128, BSTG = TBN * 128;  // bytes per stage (fp16)
@@ -478,18 +478,43 @@ __global__ __launch_bounds__(256, 2) void gemm_g64_kernel(GemmArgs a) {
 #pragma unroll
     for (int j = 1; j < D; ++j) load_regs(j, min(j, nkb - 1));
     __syncthreads();
-    for (int kb0 = 0; kb0 < nkb; kb0 += D) {
+    if constexpr (PIPE) {
+        // Two accumulator sets: step kb's MFMAs (into set kb & 1) are issued
+        // before step kb-1's epilogue (from the other set), so the matrix
+        // cores and the VALU work at once inside the wave. Epilogues still
+        // run in group order; step kb-1's scales stay in their ring slot
+        // until step kb+2 is staged.
+        float16_t acc2[2][MT][NT];
+        constexpr int U = D % 2 == 0 ? D : 2 * D;  // slots and sets both constant
+        for (int kb0 = 0; kb0 < nkb; kb0 += U) {
 #pragma unroll
-        for (int j = 0; j < D; ++j) {
-            const int kb = kb0 + j;
-            if (kb >= nkb) break;  // uniform
-            // unconditional (the last K-step is reloaded near the end), so
-            // the compiler's load counts do not depend on the path taken
-            load_regs(j, min(kb + D, nkb - 1));
-            mfma_step(kb & 1, acc);
-            epilogue(kb, acc);
-            if (kb + 1 < nkb) store_lds((kb + 1) & 1, (j + 1) % D, kb + 1);
-            __syncthreads();
+            for (int j = 0; j < U; ++j) {
+                const int kb = kb0 + j;
+                if (kb >= nkb) break;  // uniform
+                load_regs(j % D, min(kb + D, nkb - 1));
+                mfma_step(kb & 1, acc2[j & 1]);
+                if (kb > 0) epilogue(kb - 1, acc2[(j + 1) & 1]);
+                if (kb + 1 < nkb) store_lds((kb + 1) & 1, (j + 1) % D, kb + 1);
+                __syncthreads();
+            }
+        }
+        // the last step's epilogue (set (nkb - 1) & 1)
+        if ((nkb - 1) & 1) epilogue(nkb - 1, acc2[1]);
+        else epilogue(nkb - 1, acc2[0]);
+    } else {
+        for (int kb0 = 0; kb0 < nkb; kb0 += D) {
+#pragma unroll
+            for (int j = 0; j < D; ++j) {
+                const int kb = kb0 + j;
+                if (kb >= nkb) break;  // uniform
+                // unconditional (the last K-step is reloaded near the end), so
+                // the compiler's load counts do not depend on the path taken
+                load_regs(j, min(kb + D, nkb - 1));
+                mfma_step(kb & 1, acc);
+                epilogue(kb, acc);
+                if (kb + 1 < nkb) store_lds((kb + 1) & 1, (j + 1) % D, kb + 1);
+                __syncthreads();
+            }
         }
     }
 
@@ -518,18 +543,21 @@ template <int MT, int NT, bool SWIGLU>
 static hipError_t launch_g64(const GemmArgs &a, hipStream_t st) {
     // register prefetch depth: as deep as the tile's registers allow
     constexpr int D = MT * NT >= 4 ? 1 : (MT * NT == 2 ? 3 : 4);
+    // a second accumulator set (epilogue overlapped with the next MFMAs)
+    // where the registers allow it
+    constexpr bool PIPE = MT * NT <= 2;
     constexpr int TBM = 64 * MT, TBN = 64 * NT;
     const int ncols = SWIGLU ? TBN / 2 : TBN;
     dim3 grid((a.N + ncols - 1) / ncols, (a.M + TBM - 1) / TBM);
     const size_t lds = 2 * (TBM + TBN) * 128 + 3 * (TBM + TBN) * 4;
     static bool attr_set = false;  // raise the dynamic LDS limit once
     if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemm_g64_kernel<MT, NT, SWIGLU, D>),
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemm_g64_kernel<MT, NT, SWIGLU, D, PIPE>),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
         attr_set = true;
     }
-    gemm_g64_kernel<MT, NT, SWIGLU, D><<<grid, 256, lds, st>>>(a);
+    gemm_g64_kernel<MT, NT, SWIGLU, D, PIPE><<<grid, 256, lds, st>>>(a);
     return hipGetLastError();
 }
 
