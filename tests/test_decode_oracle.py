@@ -87,11 +87,12 @@ def test_fp16_conversions(orc):
     np.testing.assert_array_equal(back, hs.view(np.float16).astype(np.float32))
 
 
-def test_decode_steps_vs_reference_forward_text(orc, ref):
+@pytest.mark.parametrize("gs", [64, 32, 128])  # the exporter's group sizes (export_qwen_bin.py:371)
+def test_decode_steps_vs_reference_forward_text(orc, ref, gs):
     """Four chained decode steps of a small model: the reference's
     forward_text (fp32 caches) vs the oracle in fp32-cache mode. Logits, the
     cache rows each step writes and the greedy ids are all bit-exact."""
-    dims = dict(SMALL)
+    dims = dict(SMALL, gs=gs)
     m = make_text_model(11, dims)
     k16, v16 = make_kv_cache(12, dims, ctx=100)
     kr, vr = k16.astype(np.float32), v16.astype(np.float32)

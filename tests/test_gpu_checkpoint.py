@@ -241,3 +241,36 @@ def test_load_rejects_what_the_decode_step_cannot_serve(dev, tmp_path, small_fil
         ck.Checkpoint(p16, max_seq=256)
     with pytest.raises(q3.Q3VLError, match="max_seq"):
         ck.Checkpoint(path, max_seq=0)
+
+
+@pytest.mark.parametrize("gs", [32, 128])
+def test_load_and_decode_other_group_sizes(dev, orc, tmp_path, gs):
+    """A checkpoint exported at group 32 / 128 loads and decodes bit-exact."""
+    torch, q3, ck, _ = dev
+    from q3vl_int8 import model as qm
+    dims = dict(SMALL, layers=1, gs=gs)
+    m = make_text_model(120 + gs, dims)
+    hdr = _hdr(ck, layers=1, group_size=gs)
+    path = str(tmp_path / f"g{gs}.bin")
+    ck.write_checkpoint(path, hdr, {n: (m[w], m[s]) for n, (w, s) in PAIRS.items()})
+    arrays = dict(m)
+    arrays["rope_cos"], arrays["rope_sin"] = ck.rope_tables(hdr["rope_theta"], 128, dims["max_seq"])
+    k16, v16 = make_kv_cache(121 + gs, dims, 50)
+    ko, vo = k16.view(np.uint16).copy(), v16.view(np.uint16).copy()
+    with ck.Checkpoint(path, max_seq=dims["max_seq"]) as c:
+        assert c.model.c.gs == gs
+        kd = torch.from_numpy(k16.view(np.int16).copy()).cuda()
+        vd = torch.from_numpy(v16.view(np.int16).copy()).cuda()
+        token = 3
+        tok = torch.tensor([token], dtype=torch.int32, device="cuda")
+        pos = torch.tensor([50], dtype=torch.int32, device="cuda")
+        logits = torch.zeros(dims["vocab"], dtype=torch.float32, device="cuda")
+        ws = qm.alloc_decode_workspace(c.model)
+        for step in range(2):
+            qm.decode_step(c.model, kd, vd, tok, pos, logits, ws)
+            torch.cuda.synchronize()
+            nid, lo = orc.decode_step(dims, arrays, ko, vo, token, 50 + step, kv_fp16=True)
+            np.testing.assert_array_equal(logits.cpu().numpy().view(np.uint32), lo.view(np.uint32))
+            np.testing.assert_array_equal(kd.cpu().numpy().view(np.uint16), ko)
+            assert int(tok.item()) == nid
+            token = nid

@@ -111,6 +111,15 @@ def test_decode_position_out_of_range(dev):
     np.testing.assert_array_equal(vd.cpu().numpy(), v16.view(np.int16))
 
 
+@pytest.mark.parametrize("gs", [32, 128])
+def test_decode_other_group_sizes(dev, orc, gs):
+    """The exporter's other group sizes (export_qwen_bin.py:371): every GEMV,
+    the fused norms and the head norms at groups of 32 and 128."""
+    s = Stepper(dev, orc, dict(SMALL, layers=1, gs=gs), seed=90 + gs, ctx=100, token=9)
+    for _ in range(3):
+        s.step()
+
+
 def test_decode_three_query_heads_per_kv_head(dev, orc):
     dims = dict(SMALL, layers=1, heads=24, kv_heads=8, hidden=3072, inter=1024)
     Stepper(dev, orc, dims, seed=50, ctx=70, token=3).step()
