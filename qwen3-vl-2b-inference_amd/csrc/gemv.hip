@@ -450,11 +450,22 @@ __global__ __launch_bounds__(GEMV_MAX_THREADS) void gemv_kernel(GemvArgs a, int 
             const float inv = rcp_rn(s);
             if (tg == 0) as_l[m * Kg + g] = s;
             const float4 *xc4 = reinterpret_cast<const float4 *>(xs + xpos(16 * tid));
+            float4 xq[4];
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4) xq[q4] = xc4[q4];
 #pragma unroll
             for (int q4 = 0; q4 < 4; ++q4) {
-                const float4 v = xc4[q4];
-                qp[m][2 * q4] = quant_pair(v.x * inv, v.y * inv);
-                qp[m][2 * q4 + 1] = quant_pair(v.z * inv, v.w * inv);
+                const float4 v = xq[q4];
+                qp[m][2 * q4] = quant_pair_finite(v.x * inv, v.y * inv);
+                qp[m][2 * q4 + 1] = quant_pair_finite(v.z * inv, v.w * inv);
+            }
+            if (__builtin_expect(!__builtin_isfinite(s), 0)) {  // a non-finite group (rare)
+#pragma unroll
+                for (int q4 = 0; q4 < 4; ++q4) {
+                    const float4 v = xq[q4];
+                    qp[m][2 * q4] = quant_pair(v.x * inv, v.y * inv);
+                    qp[m][2 * q4 + 1] = quant_pair(v.z * inv, v.w * inv);
+                }
             }
         }
         lds_barrier();

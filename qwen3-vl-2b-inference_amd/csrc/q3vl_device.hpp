@@ -44,6 +44,20 @@ Q3VL_INLINE uint32_t quant_pair(float lo, float hi) {
     return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pk_i16(a, b));
 }
 
+// quant_pair for a group whose scale s is finite. Then every x of the group
+// was finite with x^2 <= the group's sum of squares, so |x / s| <= 127 *
+// sqrt(gs) * (1 + 2^-16) < 2^22: adding 1.5 * 2^23 rounds to the nearest
+// integer, ties to even (the sum lies in [2^23, 2^24), whose spacing is 1),
+// and the integer is the sum's bits less the constant's. Equal to
+// quant_pair there (its INT32_MIN cases need a non-finite q).
+Q3VL_INLINE uint32_t quant_pair_finite(float lo, float hi) {
+    constexpr float kMagic = 12582912.0f;  // 1.5 * 2^23
+    constexpr int32_t kMagicBits = 0x4B400000;
+    const int32_t a = __builtin_bit_cast(int32_t, lo + kMagic) - kMagicBits;
+    const int32_t b = __builtin_bit_cast(int32_t, hi + kMagic) - kMagicBits;
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pk_i16(a, b));
+}
+
 // Correctly rounded fp32 sqrt and reciprocal. sqrt: the compiler's IEEE
 // expansion of the fp32 square root (hardware estimate, then a one-ulp
 // correction from fma residuals), about 15 fp32 operations; it equals the

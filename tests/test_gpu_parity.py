@@ -159,6 +159,38 @@ def test_nonfinite_activation_rows_stay_nonfinite(orc):
     assert np.array_equal(np.isnan(C), np.isnan(C_ref)) and np.isnan(C).all()
 
 
+@pytest.mark.parametrize("M", [1, 3])
+def test_extreme_activation_groups(orc, M):
+    """Groups at the edges of the quantizer. Row 0 has only finite group
+    scales: squares near fp32 overflow (one element at 1.8e19, q at the
+    127 * sqrt(64) bound), 1e18 throughout a group, values at the 1e-6 floor
+    of the scale. The GEMV's fast rounding relies on that bound. Row 1 has
+    infinite scales (a square that overflows, +-inf) and row 2 a NaN: the
+    saturating path (INT32_MIN for NaN products). Bit-exact, NaN where the
+    oracle has NaN."""
+    A, W, S = make_case(6, M, 2048, 2048, 64)
+    A[0, 0:64] = 1.0e18
+    A[0, 5] = -1.7e18
+    A[0, 64:128] = 1.0
+    A[0, 70] = 1.8e19            # x^2 = 3.24e38 < FLT_MAX
+    A[0, 128:192] = 1e-30
+    A[0, 192:256] = -3.0
+    A[0, 256:320] = 2.5e-3
+    A[0, 300] = -7.0e15
+    if M > 1:
+        A[1, 0:64] = 0.5
+        A[1, 10] = 2.0e19        # x^2 overflows: infinite scale
+        A[1, 200] = np.inf
+        A[1, 330] = -np.inf
+        A[2, 384:448] = np.nan
+    C = host(q.linear_i8(dev(A), dev(W), dev(S), 64))
+    C_ref = orc.linear(A, W, S, 64)
+    assert np.isfinite(C_ref[0]).all()
+    nan = np.isnan(C_ref)
+    assert np.array_equal(np.isnan(C), nan)
+    np.testing.assert_array_equal(C[~nan].view(np.uint32), C_ref[~nan].view(np.uint32))
+
+
 # -------------------------------------------------------------- fused consumers
 @pytest.mark.parametrize("M,N,K", [(1, 6144, 2048), (1, 1024, 1024), (4, 512, 1024), (64, 512, 1024),
                                    (512, 768, 2048)])
