@@ -227,8 +227,10 @@ def export_checkpoint(path: str, hdr: dict, text: dict, vision: dict | None = No
     write_weights_streaming (export_qwen_bin.py:297-357). text: name -> fp32
     array or tensor of text_shapes(hdr)[name]."""
     import torch
-    if hdr["text_bits"] != 8:
-        write_checkpoint(path, hdr, {n: np.asarray(text[n]) for n in TEXT_TENSORS}, vision)
+    if hdr["text_bits"] != 8:  # raw values: no quantization to run
+        host = {n: (text[n].detach().cpu().numpy() if isinstance(text[n], torch.Tensor)
+                    else np.asarray(text[n])) for n in TEXT_TENSORS}
+        write_checkpoint(path, hdr, host, vision)
         return
     packed = {}
     for n in TEXT_TENSORS:

@@ -193,3 +193,28 @@ def test_oracle_quantizer_error_bound(orc):
     np.testing.assert_array_equal(np.abs(q.reshape(-1, 64)[np.arange(300), am]), 127)
     np.testing.assert_array_equal(np.sign(q.reshape(-1, 64)[np.arange(300), am]),
                                   np.sign(g[np.arange(300), am]))
+
+
+def test_writer_rejects_wrong_shapes(tmp_path, orc):
+    hdr = dict(TINY)
+    text, _ = _tiny_text(hdr, orc, 8)
+    q, sc = text["k"]
+    bad = dict(text, k=(q[:, :-1], sc))  # one row short
+    with pytest.raises(ValueError, match="k:"):
+        ck.write_checkpoint(str(tmp_path / "bad.bin"), hdr, bad)
+    bad = dict(text, k=(q, sc[:-1]))     # one scale short
+    with pytest.raises(ValueError, match="k:"):
+        ck.write_checkpoint(str(tmp_path / "bad2.bin"), hdr, bad)
+    vis = {"pos_emb_w": np.zeros((10, 8), np.float32)}
+    with pytest.raises(ValueError, match="pos_emb_w"):
+        ck.write_checkpoint(str(tmp_path / "bad3.bin"), hdr, text, vis)
+
+
+def test_raw_text_export_needs_no_device(tmp_path, orc):
+    """fp32 text weights are written as they are (no quantizer involved)."""
+    hdr = dict(TINY, text_bits=32)
+    _, floats = _tiny_text(hdr, orc, 9)
+    a, b = str(tmp_path / "a.bin"), str(tmp_path / "b.bin")
+    ck.export_checkpoint(a, hdr, floats)
+    ck.write_checkpoint(b, hdr, floats)
+    assert open(a, "rb").read() == open(b, "rb").read()
