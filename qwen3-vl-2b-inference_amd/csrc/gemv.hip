@@ -538,6 +538,28 @@ __global__ __launch_bounds__(GEMV_MAX_THREADS) void gemv_kernel(GemvArgs a, int 
                         Gd[(size_t)row_n(cur, r) * Kg + g] = tot;
                     }
                 }
+            } else if constexpr (MR == 8 && T <= 8) {
+                // the 8 activation rows' sums, reduced over the group's T
+                // threads so that thread tg holds rows tg*W .. tg*W + W-1
+                // (rows past M carry 0 and are not written)
+                constexpr int W = 8 / T;
+                int32_t p[8];
+#pragma unroll
+                for (int m = 0; m < 8; ++m) {
+                    int32_t acc = 0;
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) acc = dot2(qp[m][j], wp[j], acc);
+                    p[m] = m < M ? acc >> 8 : 0;
+                }
+                scatter_sums<T>(p, tg);
+#pragma unroll
+                for (int k = 0; k < W; ++k) {
+                    const int m = tg * W + k;
+                    if (act && m < M) {
+                        accb[(m * R + r) * ld + g] = p[k];
+                        if (Gd) Gd[((size_t)m * cur.tN + row_n(cur, r)) * Kg + g] = p[k];
+                    }
+                }
             } else {
 #pragma unroll
                 for (int m = 0; m < MR; ++m) {
