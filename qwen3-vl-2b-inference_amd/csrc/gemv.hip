@@ -538,14 +538,16 @@ __global__ __launch_bounds__(GEMV_MAX_THREADS) void gemv_kernel(GemvArgs a, int 
                         Gd[(size_t)row_n(cur, r) * Kg + g] = tot;
                     }
                 }
-            } else if constexpr (MR == 8 && T <= 8) {
-                // the 8 activation rows' sums, reduced over the group's T
-                // threads so that thread tg holds rows tg*W .. tg*W + W-1
-                // (rows past M carry 0 and are not written)
-                constexpr int W = 8 / T;
-                int32_t p[8];
+            } else if constexpr (T <= 8) {
+                // the MR activation rows' sums, reduced over the group's T
+                // threads: with MR >= T thread tg holds rows tg*W .. tg*W + W-1,
+                // with MR < T the SH threads tg of row tg / SH all hold it and
+                // the first writes it (rows past M carry 0 and are not written)
+                constexpr int W = MR >= T ? MR / T : 1;
+                constexpr int SH = MR >= T ? 1 : T / MR;
+                int32_t p[MR];
 #pragma unroll
-                for (int m = 0; m < 8; ++m) {
+                for (int m = 0; m < MR; ++m) {
                     int32_t acc = 0;
 #pragma unroll
                     for (int j = 0; j < 8; ++j) acc = dot2(qp[m][j], wp[j], acc);
@@ -554,8 +556,8 @@ __global__ __launch_bounds__(GEMV_MAX_THREADS) void gemv_kernel(GemvArgs a, int 
                 scatter_sums<T>(p, tg);
 #pragma unroll
                 for (int k = 0; k < W; ++k) {
-                    const int m = tg * W + k;
-                    if (act && m < M) {
+                    const int m = (tg / SH) * W + k;
+                    if (act && m < M && (SH == 1 || tg % SH == 0)) {
                         accb[(m * R + r) * ld + g] = p[k];
                         if (Gd) Gd[((size_t)m * cur.tN + row_n(cur, r)) * Kg + g] = p[k];
                     }

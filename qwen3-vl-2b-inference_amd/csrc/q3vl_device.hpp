@@ -178,47 +178,44 @@ Q3VL_INLINE int32_t run_sum(int32_t v) {
     return v;
 }
 
-// Reduce-scatter of 8 per-thread sums over the aligned run of T threads
-// (T = 1, 2, 4 or 8) that holds one group: thread tg of the run ends with
-// the run's totals for sums j = tg*W .. tg*W + W-1 (W = 8/T) in v[0..W).
-// Each step halves the set by one bit of tg: the thread keeps the half its
-// final sums lie in and adds its partner's copy of that half (the partner
-// differs in that bit: half mirror for bit 2, xor 2 for bit 1, xor 1 for
-// bit 0). Integer adds, so the totals equal any other summation order.
-template <int T>
-Q3VL_INLINE void scatter_sums(int32_t (&v)[8], int tg) {
+// One step of scatter_sums over n values: the thread keeps the half of
+// v[0..n) its final sums lie in (the upper half when hi) and adds the
+// partner's copy of that half; with one value left both add it whole.
+template <int n, int N, typename Dpp>
+Q3VL_INLINE void scatter_step(int32_t (&v)[N], bool hi, Dpp dpp) {
+    if constexpr (n == 1) {
+        v[0] += dpp(v[0]);
+    } else {
+        constexpr int H = n / 2;
+#pragma unroll
+        for (int k = 0; k < H; ++k) {
+            const int32_t keep = hi ? v[H + k] : v[k];
+            const int32_t send = hi ? v[k] : v[H + k];
+            v[k] = keep + dpp(send);
+        }
+    }
+}
+
+// Reduce-scatter of N per-thread sums (N = 1, 2, 4 or 8) over the aligned
+// run of T threads (T = 1, 2, 4 or 8) that holds one group. When N >= T,
+// thread tg of the run ends with the run's totals for sums
+// j = tg*W .. tg*W + W-1 (W = N/T) in v[0..W); when N < T, with the total
+// for sum j = tg / (T/N) in v[0], which the T/N threads tg of that sum all
+// hold. Each step halves the set by one bit of tg (bit 2 against the half
+// mirror, bit 1 against xor 2, bit 0 against xor 1), highest bit first.
+// Integer adds, so the totals equal any other summation order.
+template <int T, int N>
+Q3VL_INLINE void scatter_sums(int32_t (&v)[N], int tg) {
     static_assert(T == 1 || T == 2 || T == 4 || T == 8, "group run of 1, 2, 4 or 8 threads");
-    // every index below is a compile-time constant (a select over a
-    // run-time index would become compare chains)
-    if constexpr (T == 8) {
-        const bool hi = (tg & 4) != 0;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const int32_t keep = hi ? v[4 + k] : v[k];
-            const int32_t send = hi ? v[k] : v[4 + k];
-            v[k] = keep + dpp_half_mirror(send);
-        }
-    }
-    if constexpr (T >= 4) {
-        constexpr int H = T == 8 ? 2 : 4;
-        const bool hi = (tg & 2) != 0;
-#pragma unroll
-        for (int k = 0; k < H; ++k) {
-            const int32_t keep = hi ? v[H + k] : v[k];
-            const int32_t send = hi ? v[k] : v[H + k];
-            v[k] = keep + dpp_xor2(send);
-        }
-    }
-    if constexpr (T >= 2) {
-        constexpr int H = T == 8 ? 1 : T == 4 ? 2 : 4;
-        const bool hi = (tg & 1) != 0;
-#pragma unroll
-        for (int k = 0; k < H; ++k) {
-            const int32_t keep = hi ? v[H + k] : v[k];
-            const int32_t send = hi ? v[k] : v[H + k];
-            v[k] = keep + dpp_xor1(send);
-        }
-    }
+    static_assert(N == 1 || N == 2 || N == 4 || N == 8, "1, 2, 4 or 8 sums");
+    // every index is a compile-time constant (a select over a run-time
+    // index would become compare chains)
+    constexpr int n2 = N;
+    constexpr int n1 = T == 8 ? (n2 > 1 ? n2 / 2 : 1) : n2;
+    constexpr int n0 = T >= 4 ? (n1 > 1 ? n1 / 2 : 1) : n1;
+    if constexpr (T == 8) scatter_step<n2>(v, (tg & 4) != 0, [](int32_t x) { return dpp_half_mirror(x); });
+    if constexpr (T >= 4) scatter_step<n1>(v, (tg & 2) != 0, [](int32_t x) { return dpp_xor2(x); });
+    if constexpr (T >= 2) scatter_step<n0>(v, (tg & 1) != 0, [](int32_t x) { return dpp_xor1(x); });
 }
 
 }  // namespace q3vl

@@ -79,7 +79,12 @@ LANE = [(1, 1024, 1024, 64), (1, 6144, 2048, 64), (1, 2048, 6144, 64), (1, 4096,
         (1, 1028, 1024, 64), (1, 1031, 1024, 64), (1, 70000, 1024, 64)]
 GENERAL = [(1, 512, 2048, 64), (1, 2048, 512, 64), (2, 256, 512, 64), (3, 1000, 2048, 64),
            (5, 1028, 1024, 32), (8, 1000, 2048, 64), (8, 384, 6144, 64), (4, 77, 1024, 128),
-           (6, 96, 256, 16), (2, 64, 1024, 256)]
+           (6, 96, 256, 16), (2, 64, 1024, 256),
+           # every (rows, threads per group) pair of the reduce-scatter:
+           # rows 1, 2, 4, 8 against group sizes 16, 32, 64, 128
+           (1, 512, 2048, 128), (1, 256, 1024, 32), (1, 256, 512, 16), (2, 300, 1024, 128),
+           (2, 96, 512, 32), (2, 64, 512, 16), (3, 200, 1024, 32), (4, 64, 512, 16),
+           (7, 100, 1024, 128)]
 GEMM = [(9, 128, 1024, 64), (16, 384, 1024, 64), (64, 512, 2048, 64), (196, 320, 4096, 64),
         (130, 200, 1024, 32), (100, 260, 2048, 128), (512, 2048, 6144, 64)]
 
