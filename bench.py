@@ -19,15 +19,24 @@ of the step and the lm_head; M=1 lane path), at the decode step's shapes:
 achieved = algorithmic bytes (int8 weights + fp32 group scales + fp32
 activations in and out) summed over one step's GEMV launches / the summed
 kernel durations, measured as HIP-graph replays of each class of launch
-between HIP events on the replaying stream; peak = 8 TB/s HBM.
+between HIP events on the replaying stream; peak = 8 TB/s HBM. In a kernel
+trace of this command the roofline region lies between two swiglu_kernel
+dispatches (one element each; nothing else in the bench launches that
+kernel), so `bench.py --trace-summary <kernel_trace.csv>` gives the same
+per-class averages from the profiler's own durations.
 
-cpu_baseline: the reference's own forward_text (oracle/_ref, compiled from the
-reference sources; fp32 KV cache as the reference keeps it) on the same model
-and context, timed on this host's cores for a bounded number of tokens.
+cpu_baseline and every config's "cpu_reference": the reference's own code
+(oracle/_ref, compiled from the reference sources) on this host's cores,
+timed in a child process that runs BEFORE this process touches the GPU (so a
+failure there cannot take the GPU figures with it, and no GPU work competes
+with it): forward_text on the same random model and context (config 1, fp32
+KV cache as the reference keeps it), and linear() at the shapes of configs 0,
+2, 3 (M=1 and M=8) and 4, each over a bounded sample stated in its entry.
 
 Also reported under "configs": config 0 (up_proj GEMV, GB/s), config 2
 (prefill gate|up+SwiGLU and down at M=512, TOPS), config 3 (lm_head GEMV +
-argmax, M=1 and 8, GB/s), config 4 (vision-encoder linears, TOPS), the
+argmax, M=1 and 8, GB/s), config 4 (vision-encoder linears: 24 blocks of
+qkv/proj/fc1/fc2 at M=784 and the merger's fc1 and fc2 at M=196, TOPS), the
 exporter's weight quantizer on one up_proj ("export", GB/s) and, with
 --configs ...,load, the load of a full-size checkpoint file into HBM (GB/s of
 file bytes, page-cache-resident file).
@@ -37,8 +46,10 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import subprocess
 import sys
 import time
+import traceback
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "qwen3-vl-2b-inference_amd"))
@@ -52,12 +63,283 @@ INT8_PEAK_TOPS = 5000.0   # dense int8 MFMA
 FP16_PEAK_TFLOPS = 2500.0
 GS = 64
 CTX = 1024
+CPU_DECODE_TOKENS = 200   # cap on the reference decode steps of the CPU leg
+MODEL_SEED = 0xD0C0DE
+# Vision encoder (config 4): 784 patch tokens, hidden 1024, MLP 4096, 24
+# blocks; the 2x2 merger runs over 196 tokens of 4096 (fc1 4096->4096, fc2
+# 4096->2048; model/src/load_model.cpp:234-237).
+VIS_T, VIS_D, VIS_F, VIS_B = 784, 1024, 4096, 24
+VIS_SHAPES = [(3 * VIS_D, VIS_D), (VIS_D, VIS_D), (VIS_F, VIS_D), (VIS_D, VIS_F)]  # (N, K)
+MERGER_SHAPES = [(4 * VIS_D, 4 * VIS_D), (2048, 4 * VIS_D)]
 
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+def wbytes(N, K):
+    return N * K + N * (K // GS) * 4
+
+
+def cfg2_ops(M=512, K=2048, I=6144):
+    return 2 * M * (2 * I) * K + 2 * M * K * I
+
+
+def vis_block_ops():
+    return sum(2 * VIS_T * N * K for N, K in VIS_SHAPES)
+
+
+def merger_ops():
+    return sum(2 * (VIS_T // 4) * N * K for N, K in MERGER_SHAPES)
+
+
+def cfg4_ops():
+    return VIS_B * vis_block_ops() + merger_ops()
+
+
+# ===================================================================== CPU leg
+def cpu_info():
+    """CPU model, physical cores and logical CPUs of this host (lscpu, else
+    /proc/cpuinfo), and the CPUs this process may run on."""
+    info = {}
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=20).stdout
+        f = {}
+        for line in out.splitlines():
+            if ":" in line:
+                k, v = line.split(":", 1)
+                f[k.strip()] = v.strip()
+        info["model"] = f.get("Model name")
+        if f.get("Core(s) per socket") and f.get("Socket(s)"):
+            info["physical_cores"] = int(f["Core(s) per socket"]) * int(f["Socket(s)"])
+        if f.get("CPU(s)"):
+            info["logical_cpus"] = int(f["CPU(s)"])
+    except (OSError, ValueError, subprocess.SubprocessError):
+        pass
+    if not info.get("model") or not info.get("physical_cores"):
+        try:
+            cores, model, logical = set(), None, 0
+            phys = core = None
+            with open("/proc/cpuinfo") as fh:
+                for line in fh:
+                    k, _, v = line.partition(":")
+                    k, v = k.strip(), v.strip()
+                    if k == "processor":
+                        logical += 1
+                    elif k == "model name" and model is None:
+                        model = v
+                    elif k == "physical id":
+                        phys = v
+                    elif k == "core id":
+                        core = v
+                        cores.add((phys, core))
+            info.setdefault("model", model)
+            if cores:
+                info.setdefault("physical_cores", len(cores))
+            info.setdefault("logical_cpus", logical)
+        except OSError:
+            pass
+    try:
+        info["affinity_cpus"] = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        pass
+    info["omp_num_threads"] = os.environ.get("OMP_NUM_THREADS")
+    return info
+
+
+def omp_threads():
+    v = os.environ.get("OMP_NUM_THREADS")
+    if v and v.isdigit():
+        return int(v)
+    try:
+        return len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        return os.cpu_count() or 1
+
+
+def _time_calls(fn, budget_s, min_runs=1, max_runs=200):
+    """Median wall time of fn() over calls made within budget_s (after one
+    untimed call), at least min_runs of them."""
+    import numpy as np
+    fn()
+    times, t0 = [], time.perf_counter()
+    while len(times) < max_runs and (len(times) < min_runs or time.perf_counter() - t0 < budget_s):
+        t = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t)
+    return float(np.median(times)), len(times)
+
+
+def cpu_decode_tokens(ctx, max_seq, cap=CPU_DECODE_TOKENS):
+    """Timed reference decode steps that fit a cache of max_seq positions
+    after the untimed step at ctx: positions ctx+1 .. ctx+n must be < max_seq."""
+    return max(0, min(cap, max_seq - ctx - 1))
+
+
+def cpu_max_seq(ctx=CTX, cap=CPU_DECODE_TOKENS):
+    """Cache length of the CPU leg's decoder: room for the untimed step at
+    ctx and cap timed steps after it."""
+    return (ctx + 1 + cap + 7) // 8 * 8
+
+
+def cpu_leg_cfg1(ref, budget_s, ctx=CTX, max_seq=None, seed=MODEL_SEED, dims=None):
+    """forward_text of the reference on the bench's random model at context
+    ctx: one untimed step, then greedy steps for about budget_s seconds, never
+    past the cache (positions < max_seq)."""
+    from golden.gen import QWEN3VL_2B, make_kv_cache, make_text_model
+    max_seq = max_seq or cpu_max_seq(ctx)
+    dims = dict(dims or QWEN3VL_2B, max_seq=max_seq)
+    m = make_text_model(seed, dims)
+    k16, v16 = make_kv_cache(seed + 1, dims, ctx)
+    k32, v32 = k16.astype("float32"), v16.astype("float32")
+    del k16, v16
+    dec = ref.decoder(dims, m, k32, v32)
+    cap = cpu_decode_tokens(ctx, max_seq)
+    try:
+        tok = dims["vocab"] - 936
+        t0 = time.perf_counter()
+        lg = dec.step(tok, ctx)
+        first = time.perf_counter() - t0
+        n, t0 = 0, time.perf_counter()
+        while n < cap and (n == 0 or time.perf_counter() - t0 < budget_s):
+            tok = int(lg.argmax())
+            lg = dec.step(tok, ctx + 1 + n)
+            n += 1
+        el = time.perf_counter() - t0
+    finally:
+        dec.close()
+    return dict(value=n / el if n else None, unit="tok/s", n=n, seconds=el,
+                sample=f"{n} greedy decode steps of the reference forward_text (28 layers, fp32 KV "
+                       f"cache) at contexts {ctx + 1}..{ctx + n}, after one untimed step "
+                       f"({first:.2f} s)")
+
+
+def cpu_leg_linear(ref, budget_s):
+    """The reference linear() at the shapes of configs 0, 2, 3 and 4."""
+    import numpy as np
+    from golden.gen import make_case
+    out = {}
+
+    # config 0: up_proj GEMV, M=1 lane path (i8:122-224)
+    N, K = 6144, 2048
+    A, W, S = make_case(0xC0FFEE00, 1, N, K, GS)
+    med, n = _time_calls(lambda: ref.linear(A, W, S, GS), budget_s, min_runs=5)
+    algo = wbytes(N, K) + K * 4 + N * 4
+    out["cfg0_up_proj_gemv"] = dict(
+        value=algo / med / 1e9, unit="GB/s", ms=med * 1e3,
+        sample=f"{n} calls of linear() M=1 N=6144 K=2048 (median)")
+
+    # config 2: gate and up (M=512, general path i8:477-662), swiglu, down
+    M, H, I = 512, 2048, 6144
+    A, Wg, Sg = make_case(0xC0FFEE02, M, I, H, GS)
+    _, Wu, Su = make_case(0xC0FFEE12, 1, I, H, GS)
+    Ad, Wd, Sd = make_case(0xC0FFEE22, M, H, I, GS)
+
+    def cfg2():
+        g = ref.linear(A, Wg, Sg, GS)
+        u = ref.linear(A, Wu, Su, GS)
+        h = ref.swiglu(g, u)
+        ref.linear(h, Wd, Sd, GS)
+
+    med, n = _time_calls(cfg2, budget_s, min_runs=1)
+    ops = cfg2_ops(M, H, I)
+    out["cfg2_prefill_gemm"] = dict(
+        value=ops / med / 1e12, unit="TOPS", ms=med * 1e3,
+        sample=f"{n} passes of linear() gate [512x2048 -> 6144], up, swiglu, down [512x6144 -> 2048] "
+               f"(median)")
+
+    # config 3: lm_head + greedy argmax, M=1 (huge-N GEMV i8:327-455) and
+    # M=8 (general path)
+    V = 151936
+    _, Wv, Sv = make_case(0xC0FFEE03, 1, V, H, GS)
+    for M in (1, 8):
+        x = np.random.default_rng(0xC0FFEE13 + M).standard_normal((M, H), dtype=np.float32)
+
+        def cfg3():
+            lg = ref.linear(x, Wv, Sv, GS)
+            lg.argmax(axis=1)
+
+        med, n = _time_calls(cfg3, budget_s / 2, min_runs=3)
+        algo = wbytes(V, H) + M * H * 4 + M * 4
+        out[f"cfg3_lm_head_argmax_m{M}"] = dict(
+            value=algo / med / 1e9, unit="GB/s", ms=med * 1e3,
+            sample=f"{n} calls of linear() M={M} N=151936 K=2048 + argmax of each row (median)")
+    del Wv, Sv
+
+    # config 4: a sample of whole ViT blocks (each qkv, proj, fc1, fc2 at
+    # M=784 with its own weights) plus the merger's fc1 and fc2 at M=196
+    rng = np.random.default_rng(0xC0FFEE04)
+    xD = rng.standard_normal((VIS_T, VIS_D), dtype=np.float32)
+    xF = rng.standard_normal((VIS_T, VIS_F), dtype=np.float32)
+    xM = rng.standard_normal((VIS_T // 4, 4 * VIS_D), dtype=np.float32)
+    mw = [make_case(0xC0FFEE40 + j, 1, N, K, GS)[1:] for j, (N, K) in enumerate(MERGER_SHAPES)]
+    t_merger = None
+    t0 = time.perf_counter()
+    for (W, S) in mw:
+        ref.linear(xM, W, S, GS)
+    t_merger = time.perf_counter() - t0
+    blocks, t_blocks = 0, 0.0
+    while blocks < VIS_B and (blocks == 0 or t_blocks + t_merger < budget_s):
+        ws = [make_case(0xC0FFEE50 + 10 * blocks + j, 1, N, K, GS)[1:]
+              for j, (N, K) in enumerate(VIS_SHAPES)]
+        t = time.perf_counter()
+        for (N, K), (W, S) in zip(VIS_SHAPES, ws):
+            ref.linear(xF if K == VIS_F else xD, W, S, GS)
+        t_blocks += time.perf_counter() - t
+        blocks += 1
+    ops = blocks * vis_block_ops() + merger_ops()
+    out["cfg4_vision_linears"] = dict(
+        value=ops / (t_blocks + t_merger) / 1e12, unit="TOPS", ms=(t_blocks + t_merger) * 1e3,
+        sample=f"{blocks} of the 24 ViT blocks (qkv, proj, fc1, fc2 of linear() at M=784) and the "
+               f"merger's fc1 and fc2 at M=196, one pass each: {ops / 1e9:.1f} G ops")
+    return out
+
+
+def cpu_leg(args):
+    """The child process: every reference CPU figure, as one JSON object."""
+    from checkers import Reference
+    res = {"cpu": cpu_info(), "threads": omp_threads()}
+    ref = Reference.load()
+    if ref is None:
+        res["error"] = "oracle/_ref/libref_q3vl.so is not built (build() compiles it where the " \
+                       "reference sources are present)"
+        return res
+    budget = args.cpu_budget
+    if "cfg1" in args.cpu_configs:
+        try:
+            res["cfg1_decode_step"] = cpu_leg_cfg1(ref, budget)
+        except Exception as e:  # noqa: BLE001 -- reported, the other figures still run
+            res["cfg1_decode_step"] = dict(error=repr(e))
+    if "linear" in args.cpu_configs:
+        try:
+            res.update(cpu_leg_linear(ref, max(2.0, budget / 3)))
+        except Exception as e:  # noqa: BLE001
+            res["linear_error"] = repr(e)
+    return res
+
+
+def run_cpu_leg_child(args):
+    """Runs the CPU leg in a child process (this process has not touched the
+    GPU yet) and returns its JSON result, or an error record."""
+    cmd = [sys.executable, os.path.abspath(__file__), "--cpu-leg", "--cpu-budget",
+           str(args.cpu_budget), "--cpu-configs", args.cpu_configs]
+    log("bench: cpu leg (reference CPU path, child process):", " ".join(cmd[1:]))
+    t = time.perf_counter()
+    try:
+        p = subprocess.run(cmd, capture_output=True, text=True, timeout=args.cpu_timeout)
+    except subprocess.TimeoutExpired:
+        return {"error": f"cpu leg exceeded {args.cpu_timeout} s"}
+    if p.stderr:
+        log(p.stderr.rstrip()[-2000:])
+    lines = [ln for ln in p.stdout.splitlines() if ln.startswith("{")]
+    if p.returncode != 0 or not lines:
+        return {"error": f"cpu leg exited with {p.returncode}", "stdout_tail": p.stdout[-500:]}
+    res = json.loads(lines[-1])
+    log(f"bench: cpu leg done in {time.perf_counter() - t:.1f} s")
+    return res
+
+
+# =================================================================== GPU legs
 def _event_time(fn, steps, warmup):
     """ms per call of fn over `steps` calls, HIP events on the current stream."""
     import torch
@@ -121,10 +403,6 @@ def copies_for(bytes_per_copy, floor=2):
     return max(floor, int((600 << 20) // bytes_per_copy) + 1)
 
 
-def wbytes(N, K):
-    return N * K + N * (K // GS) * 4
-
-
 # ------------------------------------------------------------------ config 1
 def decode_dims(max_seq):
     from golden.gen import QWEN3VL_2B
@@ -180,18 +458,27 @@ def bench_cfg1(args, m, k16, v16, dims):
     ms = e0.elapsed_time(e1) / args.steps
     end_pos = int(pos.item())
     assert end_pos == CTX + args.warmup + args.steps, (end_pos, args.warmup, args.steps)
-    step_bytes = decode_step_weight_bytes(dims)
+    step_bytes = decode_step_bytes(dims, CTX + args.warmup + args.steps // 2)
     res = dict(name="cfg1_decode_step", metric="tok/s", value=1000.0 / ms, ms=ms,
                eager_ms=eager_ms, contexts=[CTX + args.warmup, end_pos - 1],
-               weight_bytes_per_token=step_bytes,
-               effective_weight_GBs=step_bytes / (ms * 1e-3) / 1e9)
+               bytes_per_token=step_bytes, bytes_roofline_tok_s=HBM_PEAK_GBS * 1e9 / step_bytes,
+               frac_of_bytes_roofline=(1000.0 / ms) / (HBM_PEAK_GBS * 1e9 / step_bytes),
+               kernel_launches_per_token=decode_launches(dims))
+    del g
     res["gemv_roofline"] = decode_gemv_roofline(model, dims)
     return res
 
 
+def decode_launches(dims):
+    """Kernel launches of one q3vl_decode_step: embedding, per layer q|k|v
+    GEMV, two attention kernels, o, gate|up and down GEMVs, then the lm_head
+    GEMV and the argmax reduction."""
+    return 1 + 6 * dims["layers"] + 2
+
+
 def decode_gemv_shapes(dims):
-    """(name, segments [(N, K)], activation K, outputs N, extra bytes) per
-    GEMV launch of one decode step, as q3vl_decode_step issues them."""
+    """(name, segments [(N, K)]) per GEMV launch of one decode step, as
+    q3vl_decode_step issues them."""
     H, I, V = dims["hidden"], dims["inter"], dims["vocab"]
     QD, KD = dims["heads"] * dims["head_dim"], dims["kv_heads"] * dims["head_dim"]
     per_layer = [("qkv", [(QD, H), (KD, H), (KD, H)]), ("o", [(H, QD)]),
@@ -199,10 +486,14 @@ def decode_gemv_shapes(dims):
     return per_layer, ("lm_head", [(V, H)])
 
 
-def decode_step_weight_bytes(dims):
+def decode_step_bytes(dims, ctx):
+    """HBM bytes one decode step must move at context ctx: every weight and
+    scale once, the KV cache rows 0..ctx read (fp16) and one row written."""
     per_layer, head = decode_gemv_shapes(dims)
     b = sum(wbytes(N, K) for _, segs in per_layer for N, K in segs) * dims["layers"]
-    return b + sum(wbytes(N, K) for N, K in head[1])
+    b += sum(wbytes(N, K) for N, K in head[1])
+    kv_row = dims["kv_heads"] * dims["head_dim"] * 2
+    return b + dims["layers"] * 2 * kv_row * (ctx + 1)
 
 
 def decode_gemv_roofline(model, dims):
@@ -210,9 +501,10 @@ def decode_gemv_roofline(model, dims):
     weights (the lm_head in plain mode). Each class of launch (qkv, o,
     gate/up, down over the 28 layers; lm_head four times) is captured in a
     HIP graph and replayed between HIP events on the capturing stream, so
-    launch gaps vanish and time / launches is the average kernel duration
-    (median of five timed trials).
-    achieved = one step's algorithmic bytes / one step's summed durations."""
+    time / launches is the average kernel duration (median of five timed
+    trials). achieved = one step's algorithmic bytes / one step's summed
+    durations. The region is delimited by two one-element swiglu launches,
+    its markers in a kernel trace."""
     import torch
     import q3vl_int8 as q
     t = model.t
@@ -240,7 +532,7 @@ def decode_gemv_roofline(model, dims):
                     wbytes(V, H) + H * 4 + V * 4),
     }
     per_step = {"qkv": L, "o": L, "gate_up": L, "down": L, "lm_head": 1}
-    res = {}
+    graphs = {}
     for name, (fns, nbytes) in kinds.items():
         for fn in fns:  # eager pass: first use
             fn()
@@ -251,7 +543,14 @@ def decode_gemv_roofline(model, dims):
                 fn()
         g.replay()
         torch.cuda.synchronize()
-        st = torch.cuda.current_stream()
+        graphs[name] = g
+    marker = torch.zeros(1, dtype=torch.float32, device="cuda")
+    q.swiglu(marker, marker)  # region start (kernel-trace marker)
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream()
+    res = {}
+    for name, (fns, nbytes) in kinds.items():
+        g = graphs[name]
         reps, trials = 5, []
         for _ in range(5):  # median of 5 timed trials of 5 replays each
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -262,43 +561,18 @@ def decode_gemv_roofline(model, dims):
             torch.cuda.synchronize()
             trials.append(e0.elapsed_time(e1) * 1e3 / (reps * len(fns)))
         us = sorted(trials)[len(trials) // 2]
-        res[name] = dict(us=us, bytes=nbytes, GBs=nbytes / (us * 1e-6) / 1e9)
+        res[name] = dict(us=us, bytes=nbytes, GBs=nbytes / (us * 1e-6) / 1e9,
+                         launches_timed=25 * len(fns))
+    q.swiglu(marker, marker)  # region end
+    torch.cuda.synchronize()
     step_us = sum(res[k]["us"] * n for k, n in per_step.items())
     step_bytes = sum(res[k]["bytes"] * n for k, n in per_step.items())
     launches = sum(per_step.values())
     gbs = step_bytes / (step_us * 1e-6) / 1e9
-    return dict(kernel="gemv_kernel<64, 1, true, R> (R = rows per tile: 2, 4 or 8 by shape)", launches=launches,
+    return dict(kernel="gemv_kernel<64, 1, true, R, KC, MD> (the decode step's GEMV launches)",
+                launches=launches,
                 bytes_per_launch=step_bytes / launches, avg_launch_us=step_us / launches,
                 achieved_GBs=gbs, frac=gbs / HBM_PEAK_GBS, step_gemv_us=step_us, by_class=res)
-
-
-def cpu_baseline_cfg1(m, k16, v16, dims, budget_s):
-    """forward_text of the reference (oracle/_ref) on the same model at the
-    same context: tokens for about budget_s seconds, one thread per core the
-    OpenMP runtime uses."""
-    from checkers import Reference
-    ref = Reference.load()
-    if ref is None:
-        return None
-    k32, v32 = k16.astype("float32"), v16.astype("float32")
-    dec = ref.decoder(dims, m, k32, v32)
-    try:
-        tok = dims["vocab"] - 936
-        t0 = time.perf_counter()
-        lg = dec.step(tok, CTX)
-        first = time.perf_counter() - t0
-        n, t0 = 0, time.perf_counter()
-        while time.perf_counter() - t0 < budget_s and n < 200:
-            tok = int(lg.argmax())
-            lg = dec.step(tok, CTX + 1 + n)
-            n += 1
-        el = time.perf_counter() - t0
-    finally:
-        dec.close()
-    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    return dict(value=n / el, unit="tok/s", cores=threads, kind="reference",
-                sample=f"{n} greedy decode steps of forward_text (28 layers, fp32 KV cache) at "
-                       f"contexts {CTX + 1}..{CTX + n}, after one untimed step ({first:.2f} s)")
 
 
 # ------------------------------------------------------------- configs 0,2,3,4
@@ -321,7 +595,7 @@ def bench_cfg0(args):
     return dict(name="cfg0_up_proj_gemv", metric="GB/s", value=gbs, ms=ms, eager_ms=eager_ms,
                 algo_bytes=algo, frac=gbs / HBM_PEAK_GBS, copies=n,
                 timing="HIP-graph replay of one launch per weight copy (eager_ms: per Python call)",
-                kernel="gemv_kernel<64, 1, true, 4>")
+                kernel="gemv_kernel<64, 1, true, 4, 2048, 0>")
 
 
 def bench_cfg2(args):
@@ -341,7 +615,7 @@ def bench_cfg2(args):
         q.linear_i8(H, Wd[0], Sd[0], GS, out=D, workspace=ws)
 
     ms = _event_time(step, max(args.steps // 2, 50), 5)
-    ops = 2 * M * (2 * I) * K + 2 * M * K * I
+    ops = cfg2_ops(M, K, I)
     tops = ops / (ms * 1e-3) / 1e12
     return dict(name="cfg2_prefill_gemm", metric="TOPS", value=tops, ms=ms, algo_ops=ops,
                 frac=tops / FP16_PEAK_TFLOPS, frac_of_int8_peak=tops / INT8_PEAK_TOPS,
@@ -369,34 +643,36 @@ def bench_cfg3(args, M):
 
 def bench_cfg4(args):
     """24 ViT blocks (qkv, proj, fc1, fc2 over 784 patch tokens) and the 2x2
-    merger projection (196 tokens): every int8 GEMM of the vision encoder
-    with its own random weights."""
+    merger's fc1 and fc2 (196 tokens of 4096): every int8 GEMM of the vision
+    encoder with its own random weights."""
     import torch
     import q3vl_int8 as q
-    T, D, F, B = 784, 1024, 4096, 24
-    shapes = [(3 * D, D), (D, D), (F, D), (D, F)]
-    Wb = [[gen_weights(N, K, 1, 7000 + 10 * b + j) for j, (N, K) in enumerate(shapes)]
+    T, D, F, B = VIS_T, VIS_D, VIS_F, VIS_B
+    Wb = [[gen_weights(N, K, 1, 7000 + 10 * b + j) for j, (N, K) in enumerate(VIS_SHAPES)]
           for b in range(B)]
-    Wm, Sm = gen_weights(2048, 4 * D, 1, 7999)
+    Wm = [gen_weights(N, K, 1, 7990 + j) for j, (N, K) in enumerate(MERGER_SHAPES)]
     xD = torch.randn((T, D), dtype=torch.float32, device="cuda")
     xF = torch.randn((T, F), dtype=torch.float32, device="cuda")
     xM = torch.randn((T // 4, 4 * D), dtype=torch.float32, device="cuda")
-    outs = {N: torch.empty((T, N), dtype=torch.float32, device="cuda") for N, _ in shapes}
-    outM = torch.empty((T // 4, 2048), dtype=torch.float32, device="cuda")
+    outs = {N: torch.empty((T, N), dtype=torch.float32, device="cuda") for N, _ in VIS_SHAPES}
+    outM = {N: torch.empty((T // 4, N), dtype=torch.float32, device="cuda") for N, _ in MERGER_SHAPES}
     ws = q.alloc_workspace(T, 3 * D, F, GS)
 
     def step(i):
         for b in range(B):
-            for j, (N, K) in enumerate(shapes):
+            for j, (N, K) in enumerate(VIS_SHAPES):
                 (W,), (S,) = Wb[b][j]
                 q.linear_i8(xF if K == F else xD, W, S, GS, out=outs[N], workspace=ws)
-        q.linear_i8(xM, Wm[0], Sm[0], GS, out=outM, workspace=ws)
+        for j, (N, K) in enumerate(MERGER_SHAPES):
+            (W,), (S,) = Wm[j]
+            q.linear_i8(xM, W, S, GS, out=outM[N], workspace=ws)
 
     ms = _event_time(step, max(args.steps // 20, 10), 2)
-    ops = B * sum(2 * T * N * K for N, K in shapes) + 2 * (T // 4) * 2048 * 4 * D
+    ops = cfg4_ops()
     tops = ops / (ms * 1e-3) / 1e12
     return dict(name="cfg4_vision_linears", metric="TOPS", value=tops, ms=ms, algo_ops=ops,
-                frac=tops / FP16_PEAK_TFLOPS, frac_of_int8_peak=tops / INT8_PEAK_TOPS, gemms=B * 4 + 1,
+                frac=tops / FP16_PEAK_TFLOPS, frac_of_int8_peak=tops / INT8_PEAK_TOPS,
+                gemms=B * len(VIS_SHAPES) + len(MERGER_SHAPES),
                 kernel="quantize_rows_kernel + gemm_g64_kernel<MT, NT, SWIGLU, D>")
 
 
@@ -472,28 +748,6 @@ def bench_load(args):
                      "the page cache, host-to-device copies, RoPE tables for 4096 rows)")
 
 
-def cpu_baseline_cfg0(budget_s):
-    """The reference's linear() (oracle/_ref) on config 0's shape."""
-    import numpy as np
-    from checkers import Reference
-    from golden.gen import make_case
-    ref = Reference.load()
-    if ref is None:
-        return None
-    N, K = 6144, 2048
-    A, W, S = make_case(0xC0FFEE00, 1, N, K, GS)
-    ref.linear(A, W, S, GS)
-    t0, times = time.perf_counter(), []
-    while time.perf_counter() - t0 < budget_s:
-        t = time.perf_counter()
-        ref.linear(A, W, S, GS)
-        times.append(time.perf_counter() - t)
-    med = float(np.median(times))
-    algo = wbytes(N, K) + K * 4 + N * 4
-    return dict(value=algo / med / 1e9, unit="GB/s", cores=int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1)),
-                kind="reference", sample=f"{len(times)} calls of linear() M=1 N=6144 K=2048, median {med * 1e3:.3f} ms")
-
-
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_gemv_traffic.json")
 
 
@@ -512,7 +766,7 @@ def pmc_workload():
     torch.add(src, 1, out=dst)
     torch.cuda.synchronize()
     dims = decode_dims(max_seq=CTX + 16)
-    m, k16, v16 = build_model(dims, 0xD0C0DE)
+    m, k16, v16 = build_model(dims, MODEL_SEED)
     model = qm.DeviceTextModel(dims, m)
     kd = torch.from_numpy(k16.view("int16")).cuda()
     vd = torch.from_numpy(v16.view("int16")).cuda()
@@ -535,6 +789,41 @@ def load_traffic():
         return None
 
 
+# ============================================================ trace summary
+def trace_summary(path):
+    """Per-kernel dispatch counts and average durations from a rocprofv3
+    kernel trace (CSV), over the whole run and inside the GEMV roofline region
+    (between the two swiglu_kernel marker dispatches), grouped by kernel name
+    and grid size."""
+    import csv
+    rows = []
+    with open(path, newline="") as f:
+        for r in csv.DictReader(f):
+            name = r.get("Kernel_Name") or r.get("KernelName") or ""
+            try:
+                t0, t1 = int(r["Start_Timestamp"]), int(r["End_Timestamp"])
+            except (KeyError, ValueError):
+                continue
+            grid = "x".join(r.get(k, "?") for k in ("Grid_Size_X", "Grid_Size_Y"))
+            rows.append((t0, t1, name, grid))
+    rows.sort()
+    marks = [i for i, r in enumerate(rows) if "swiglu_kernel" in r[2]]
+    region = rows[marks[0] + 1:marks[1]] if len(marks) >= 2 else []
+
+    def agg(rs):
+        d = {}
+        for t0, t1, name, grid in rs:
+            e = d.setdefault(f"{name} [{grid}]", [0, 0.0])
+            e[0] += 1
+            e[1] += (t1 - t0) / 1000.0
+        return {k: dict(calls=c, avg_us=round(tot / c, 3), total_us=round(tot, 1))
+                for k, (c, tot) in sorted(d.items(), key=lambda kv: -kv[1][1])}
+
+    return dict(trace=path, dispatches=len(rows), markers=len(marks),
+                roofline_region=agg(region), whole_run=agg(rows))
+
+
+# ===================================================================== main
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -542,14 +831,31 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--configs", default="cfg1,cfg0,cfg2,cfg3,cfg4,export")
     ap.add_argument("--cpu-budget", type=float, default=15.0,
-                    help="seconds of reference CPU decode for cpu_baseline (0: skip)")
+                    help="seconds of reference CPU decode for cpu_baseline; the linear() "
+                         "figures get a third of it each (0: skip the CPU leg)")
+    ap.add_argument("--cpu-configs", default="cfg1,linear",
+                    help="CPU figures to time: cfg1 (forward_text), linear (configs 0, 2, 3, 4)")
+    ap.add_argument("--cpu-timeout", type=float, default=300.0)
+    ap.add_argument("--cpu-leg", action="store_true",
+                    help="(internal) run only the reference CPU leg and print its JSON")
     ap.add_argument("--pmc-workload", action="store_true",
                     help="run only the workload of the HBM-traffic counter passes")
+    ap.add_argument("--trace-summary", metavar="KERNEL_TRACE_CSV",
+                    help="summarize a rocprofv3 kernel trace of this bench and exit")
     args = ap.parse_args()
+    if args.trace_summary:
+        print(json.dumps(trace_summary(args.trace_summary), indent=1))
+        return
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (see the sharding "
               "notes in the design document); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
+    if args.cpu_leg:
+        print(json.dumps(cpu_leg(args)), flush=True)
+        return
+    # The CPU leg first, in a child process, before this process touches the GPU.
+    cpu_res = run_cpu_leg_child(args) if args.cpu_budget > 0 and not args.pmc_workload else None
+
     import torch
     import q3vl_int8 as q
     q.lib()  # fails loudly if the HIP library is missing
@@ -559,48 +865,71 @@ def main():
         return
     configs = args.configs.split(",")
     dims = decode_dims(max_seq=(CTX + args.warmup + args.steps + 7 + 15) // 8 * 8)
-    results, cpu, m = [], None, None
+    results = []
+    runners = {
+        "cfg0": lambda: [bench_cfg0(args)],
+        "cfg2": lambda: [bench_cfg2(args)],
+        "cfg3": lambda: [bench_cfg3(args, 1), bench_cfg3(args, 8)],
+        "cfg4": lambda: [bench_cfg4(args)],
+        "export": lambda: [bench_export(args)],
+        "load": lambda: [bench_load(args)],
+    }
+    for c in configs:
+        if c != "cfg1" and c not in runners:
+            raise SystemExit(f"unknown config {c!r} (cfg0..cfg4, export, load)")
     for c in configs:
         log("bench:", c)
-        if c == "cfg1":
-            m, k16, v16 = build_model(dims, 0xD0C0DE)
-            results.append(bench_cfg1(args, m, k16, v16, dims))
-        elif c == "cfg0":
-            results.append(bench_cfg0(args))
-        elif c == "cfg2":
-            results.append(bench_cfg2(args))
-        elif c == "cfg3":
-            results.append(bench_cfg3(args, 1))
-            results.append(bench_cfg3(args, 8))
-        elif c == "cfg4":
-            results.append(bench_cfg4(args))
-        elif c == "export":
-            results.append(bench_export(args))
-        elif c == "load":
-            results.append(bench_load(args))
-        else:
-            raise SystemExit(f"unknown config {c!r} (cfg0..cfg4, export, load)")
+        try:
+            if c == "cfg1":
+                m, k16, v16 = build_model(dims, MODEL_SEED)
+                out = [bench_cfg1(args, m, k16, v16, dims)]
+                del m, k16, v16
+            else:
+                out = runners[c]()
+        except Exception as e:  # noqa: BLE001 -- one config's failure is recorded, not fatal
+            traceback.print_exc()
+            out = [dict(name=c, error=repr(e))]
         torch.cuda.synchronize()
-        log(json.dumps(results[-1]))
+        for r in out:
+            log(json.dumps(r))
+        results.extend(out)
+        torch.cuda.empty_cache()
     by = {r["name"]: r for r in results}
     head = by.get("cfg1_decode_step")
     if head is None:
         raise SystemExit("the headline needs cfg1 in --configs")
-    if args.cpu_budget > 0:
-        log("bench: cpu baseline (reference forward_text)")
-        cpu = cpu_baseline_cfg1(m, k16, v16, dims, args.cpu_budget)
-        if "cfg0_up_proj_gemv" in by:
-            by["cfg0_up_proj_gemv"]["cpu_reference"] = cpu_baseline_cfg0(min(5.0, args.cpu_budget))
-    rf = head["gemv_roofline"]
+
+    cpu = None
+    if cpu_res is not None:
+        threads = cpu_res.get("threads")
+        info = cpu_res.get("cpu", {})
+        c1 = cpu_res.get("cfg1_decode_step")
+        if c1 and c1.get("value"):
+            cpu = dict(value=round(c1["value"], 3), unit="tok/s", cores=threads, kind="reference",
+                       sample=c1["sample"], cpu_model=info.get("model"),
+                       physical_cores=info.get("physical_cores"),
+                       logical_cpus=info.get("logical_cpus"))
+        else:
+            cpu = dict(value=None, unit="tok/s", cores=threads, kind="reference",
+                       error=(c1 or {}).get("error") or cpu_res.get("error"))
+        for name, r in by.items():
+            cr = cpu_res.get(name)
+            if cr:
+                r["cpu_reference"] = dict(cr, cores=threads, kind="reference",
+                                          cpu_model=info.get("model"))
+                if cr.get("value") and r.get("value"):
+                    r["gpu_over_cpu"] = round(r["value"] / cr["value"], 1)
+
+    rf = head.get("gemv_roofline") if "error" not in head else None
     tr = load_traffic()
     line = {
         "metric": "decode tok/s, Qwen3-VL-2B text decoder (int8 group-64 weights), 1 GPU",
-        "value": round(head["value"], 2),
+        "value": round(head["value"], 2) if "value" in head else None,
         "unit": "tok/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(head["ms"], 4),
+        "ms_per_step": round(head["ms"], 4) if "ms" in head else None,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -611,14 +940,16 @@ def main():
                                "intermediate 6144, vocab 151936, group 64, fp16 KV at context 1024, "
                                "batch 1, HIP graph per step",
                    "global_batch": 1, "context": CTX},
-        "roofline": {"bound": "hbm", "achieved": round(rf["achieved_GBs"], 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(rf["frac"], 4),
-                     "traffic": round(tr["hbm_bytes_per_launch"]) if tr else None,
-                     "kernel": rf["kernel"], "bytes_per_launch": round(rf["bytes_per_launch"]),
-                     "avg_launch_us": round(rf["avg_launch_us"], 3)},
+        "roofline": ({"bound": "hbm", "achieved": round(rf["achieved_GBs"], 1), "peak": HBM_PEAK_GBS,
+                      "unit": "GB/s", "frac": round(rf["frac"], 4),
+                      "traffic": round(tr["hbm_bytes_per_launch"]) if tr else None,
+                      "kernel": rf["kernel"], "bytes_per_launch": round(rf["bytes_per_launch"]),
+                      "avg_launch_us": round(rf["avg_launch_us"], 3)} if rf else None),
         "cpu_baseline": cpu,
         "configs": {r["name"]: {k: v for k, v in r.items() if k != "name"} for r in results},
     }
+    if "error" in head:
+        line["error"] = head["error"]
     print(json.dumps(line), flush=True)
 
 

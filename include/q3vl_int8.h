@@ -62,7 +62,8 @@ enum q3vl_status {
     Q3VL_ERR_INVALID_ARGUMENT = 1, /* null / misaligned pointer, bad shape   */
     Q3VL_ERR_UNSUPPORTED = 2,      /* dtype combination or shape not served  */
     Q3VL_ERR_HIP = 3,              /* a HIP runtime call failed              */
-    Q3VL_ERR_OUT_OF_MEMORY = 4     /* workspace or registry allocation failed */
+    Q3VL_ERR_OUT_OF_MEMORY = 4,    /* workspace or registry allocation failed */
+    Q3VL_ERR_STALE_WEIGHT = 5      /* registry entry no longer matches host  */
 };
 
 /* DType values of the reference (utils/include/tensor.hpp:38). */
@@ -78,7 +79,7 @@ enum q3vl_dtype {
 const char *q3vl_last_error(void);
 /* ABI version of this header (bumped on any signature change). */
 int q3vl_abi_version(void);
-#define Q3VL_ABI_VERSION 1
+#define Q3VL_ABI_VERSION 2
 
 /* Scratch bytes needed by q3vl_linear_i8* / q3vl_lm_head_argmax for a shape. */
 size_t q3vl_workspace_bytes(size_t M, size_t N, size_t K, size_t group_size);
@@ -264,14 +265,27 @@ int q3vl_quantize_groupwise(const float *x, size_t count, size_t group, int8_t *
 /* ---- weight registry for host-pointer callers (the drop-in linear()).
  * The reference hands linear() mmapped host pointers to weights and scales
  * (model/src/load_model.cpp:146-181); the registry uploads a weight once and
- * maps its host address to device copies (256-byte aligned). */
+ * maps its host address to device copies (256-byte aligned).
+ *
+ * An entry is identified by host_W together with host_S, N, K, group_size
+ * and a fingerprint of the host bytes (64-bit hash over the first and last
+ * 256 bytes of W, 16 strided 64-byte samples of it, and the first and last
+ * 64 bytes of S). q3vl_weight_register returns the existing copies when all
+ * of these match; when host_W is registered with anything else (the engine
+ * unmapped one model and mapped another at the same address, or passes
+ * another shape) it frees the old copies and uploads the new weight. The
+ * fingerprint is a sampled check: a caller that replaces weights in place
+ * releases them (q3vl_weight_release) before the next call. */
 int q3vl_weight_register(const int8_t *host_W, const float *host_S, size_t N,
                          size_t K, size_t group_size, const int8_t **dev_W,
                          const float **dev_S);
-/* Device copies of a registered host weight; Q3VL_ERR_INVALID_ARGUMENT if
- * host_W is not registered. */
-int q3vl_weight_lookup(const void *host_W, const int8_t **dev_W,
-                       const float **dev_S);
+/* Device copies of a registered host weight. Q3VL_OK only if host_W is
+ * registered with the same host_S, N, K, group_size and fingerprint;
+ * Q3VL_ERR_INVALID_ARGUMENT if host_W is not registered;
+ * Q3VL_ERR_STALE_WEIGHT if it is registered with any of them different (the
+ * caller re-registers; nothing is returned). */
+int q3vl_weight_lookup(const void *host_W, const float *host_S, size_t N, size_t K,
+                       size_t group_size, const int8_t **dev_W, const float **dev_S);
 int q3vl_weight_release(const void *host_W);
 int q3vl_weight_release_all(void);
 

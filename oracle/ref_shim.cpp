@@ -230,12 +230,18 @@ void *ref_decoder_create(const ref_model_desc *d, float *k_cache, float *v_cache
     return r;
 }
 
-// forward_text for a text token at pos; logits [vocab] copied out.
-void ref_decoder_step(void *h, int token, size_t pos, float *logits) {
+// forward_text for a text token at pos; logits [vocab] copied out. Returns 0,
+// or -1 without calling forward_text when pos is outside the caches
+// (pos >= max_seq) or the token outside the vocabulary: forward_text checks
+// neither and would write the K/V cache rows at pos and att[h * S + t] past
+// the buffers (model/src/forward.cpp:550-584).
+int ref_decoder_step(void *h, int token, size_t pos, float *logits) {
     auto *r = static_cast<RefDecoder *>(h);
+    if (pos >= (size_t)r->cfg.seq_len || token < 0 || token >= r->cfg.vocab_size) return -1;
     Silence quiet;
     const float *out = forward_text(&r->cfg, &r->st, &r->w, token, pos);
     memcpy(logits, out, r->logits.size() * 4);
+    return 0;
 }
 
 void ref_decoder_destroy(void *h) {

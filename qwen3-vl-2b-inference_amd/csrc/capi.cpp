@@ -248,10 +248,51 @@ int run_linear(const float *A, int nseg, const int8_t *const *W, const float *co
 struct RegEntry {
     void *dW = nullptr;
     void *dS = nullptr;
+    const float *hS = nullptr;
     size_t N = 0, K = 0, gs = 0;
+    uint64_t fp = 0;
 };
 std::mutex g_reg_mu;
 std::unordered_map<const void *, RegEntry> g_reg;
+
+// FNV-1a over byte ranges.
+uint64_t fnv1a(uint64_t h, const unsigned char *p, size_t n) {
+    for (size_t i = 0; i < n; ++i) {
+        h ^= p[i];
+        h *= 0x100000001b3ull;
+    }
+    return h;
+}
+
+// Sampled fingerprint of a host weight: the first and last 256 bytes of W,
+// 16 strided 64-byte samples of it, the first and last 64 bytes of S.
+uint64_t weight_fingerprint(const int8_t *W, const float *S, size_t N, size_t K, size_t gs) {
+    const auto *w = reinterpret_cast<const unsigned char *>(W);
+    const auto *s = reinterpret_cast<const unsigned char *>(S);
+    const size_t wb = N * K, sb = gs ? N * (K / gs) * 4 : 0;
+    uint64_t h = 0xcbf29ce484222325ull;
+    auto take = [&](const unsigned char *base, size_t total, size_t off, size_t n) {
+        if (off >= total) return;
+        if (n > total - off) n = total - off;
+        h = fnv1a(h, base + off, n);
+    };
+    take(w, wb, 0, 256);
+    take(w, wb, wb > 256 ? wb - 256 : 0, 256);
+    for (size_t i = 1; i <= 16; ++i) take(w, wb, wb / 17 * i, 64);
+    take(s, sb, 0, 64);
+    take(s, sb, sb > 64 ? sb - 64 : 0, 64);
+    return h;
+}
+
+bool reg_matches(const RegEntry &e, const float *host_S, size_t N, size_t K, size_t gs, uint64_t fp) {
+    return e.hS == host_S && e.N == N && e.K == K && e.gs == gs && e.fp == fp;
+}
+
+void reg_free(RegEntry &e) {
+    (void)hipFree(e.dW);
+    (void)hipFree(e.dS);
+    e.dW = e.dS = nullptr;
+}
 
 // ------------------------------------------------------------ decode step
 struct DecodeLayout {
@@ -327,6 +368,9 @@ int check_model(const q3vl_text_model *m) {
             return fail(Q3VL_ERR_INVALID_ARGUMENT, "norm weights must be 8-byte aligned");
     return Q3VL_OK;
 }
+
+int decode_step_on(const q3vl_text_model *m, uint16_t *k_cache, uint16_t *v_cache,
+                   int32_t *token, int32_t *pos, float *logits, char *w, hipStream_t st);
 
 GemvArgs gemv1(const float *A, int K, int gs) {
     GemvArgs a{};
@@ -485,7 +529,17 @@ int q3vl_decode_step(const q3vl_text_model *m, uint16_t *k_cache, uint16_t *v_ca
     char *w = nullptr;
     rc = resolve_ws(workspace, workspace_bytes, L.total, &w);
     if (rc) return rc;
-    hipStream_t st = (hipStream_t)stream;
+    return decode_step_on(m, k_cache, v_cache, token, pos, logits, w, (hipStream_t)stream);
+}
+
+}  // extern "C"
+
+namespace {
+
+// The decode step's launches over a resolved workspace w (decode_layout(m)).
+int decode_step_on(const q3vl_text_model *m, uint16_t *k_cache, uint16_t *v_cache,
+                   int32_t *token, int32_t *pos, float *logits, char *w, hipStream_t st) {
+    const DecodeLayout L = decode_layout(m);
     const int H = m->hidden, I = m->intermediate, NH = m->heads, NKV = m->kv_heads;
     const int D = m->head_dim, gs = m->group_size, V = m->vocab;
     const int QD = NH * D, KD = NKV * D;
@@ -575,22 +629,32 @@ int q3vl_decode_step(const q3vl_text_model *m, uint16_t *k_cache, uint16_t *v_ca
     return Q3VL_OK;
 }
 
+}  // namespace
+
+extern "C" {
+
 int q3vl_weight_register(const int8_t *host_W, const float *host_S, size_t N, size_t K,
                          size_t group_size, const int8_t **dev_W, const float **dev_S) {
     if (!host_W || !host_S || !group_size || K % group_size)
         return fail(Q3VL_ERR_INVALID_ARGUMENT, "bad weight registration arguments");
+    const uint64_t fp = weight_fingerprint(host_W, host_S, N, K, group_size);
     std::lock_guard<std::mutex> lk(g_reg_mu);
     auto it = g_reg.find(host_W);
-    if (it != g_reg.end()) {
-        const RegEntry &e = it->second;
-        if (e.N != N || e.K != K || e.gs != group_size)
-            return fail(Q3VL_ERR_INVALID_ARGUMENT,
-                        "host weight %p already registered with another shape", (const void *)host_W);
-    } else {
+    if (it != g_reg.end() && !reg_matches(it->second, host_S, N, K, group_size, fp)) {
+        // A stale entry (another weight now lives at host_W): work queued on
+        // any stream may still read the old copies.
+        Q3VL_HIP(hipDeviceSynchronize(), "hipDeviceSynchronize");
+        reg_free(it->second);
+        g_reg.erase(it);
+        it = g_reg.end();
+    }
+    if (it == g_reg.end()) {
         RegEntry e;
+        e.hS = host_S;
         e.N = N;
         e.K = K;
         e.gs = group_size;
+        e.fp = fp;
         const size_t wb = N * K, sb = N * (K / group_size) * 4;
         if (hipMalloc(&e.dW, wb ? wb : 1) != hipSuccess ||
             hipMalloc(&e.dS, sb ? sb : 1) != hipSuccess) {
@@ -600,8 +664,7 @@ int q3vl_weight_register(const int8_t *host_W, const float *host_S, size_t N, si
         hipError_t err = hipMemcpy(e.dW, host_W, wb, hipMemcpyHostToDevice);
         if (err == hipSuccess) err = hipMemcpy(e.dS, host_S, sb, hipMemcpyHostToDevice);
         if (err != hipSuccess) {
-            (void)hipFree(e.dW);
-            (void)hipFree(e.dS);
+            reg_free(e);
             return hip_fail(err, "weight upload");
         }
         it = g_reg.emplace(host_W, e).first;
@@ -611,13 +674,25 @@ int q3vl_weight_register(const int8_t *host_W, const float *host_S, size_t N, si
     return Q3VL_OK;
 }
 
-int q3vl_weight_lookup(const void *host_W, const int8_t **dev_W, const float **dev_S) {
+int q3vl_weight_lookup(const void *host_W, const float *host_S, size_t N, size_t K,
+                       size_t group_size, const int8_t **dev_W, const float **dev_S) {
+    if (!host_W || !host_S || !group_size || K % group_size)
+        return fail(Q3VL_ERR_INVALID_ARGUMENT, "bad weight lookup arguments");
+    const uint64_t fp =
+        weight_fingerprint(static_cast<const int8_t *>(host_W), host_S, N, K, group_size);
     std::lock_guard<std::mutex> lk(g_reg_mu);
     auto it = g_reg.find(host_W);
     if (it == g_reg.end())
         return fail(Q3VL_ERR_INVALID_ARGUMENT, "host weight %p is not registered", host_W);
-    if (dev_W) *dev_W = static_cast<const int8_t *>(it->second.dW);
-    if (dev_S) *dev_S = static_cast<const float *>(it->second.dS);
+    const RegEntry &e = it->second;
+    if (!reg_matches(e, host_S, N, K, group_size, fp))
+        return fail(Q3VL_ERR_STALE_WEIGHT,
+                    "host weight %p is registered as [%zu x %zu] group %zu with scales %p; called "
+                    "with [%zu x %zu] group %zu, scales %p%s",
+                    host_W, e.N, e.K, e.gs, (const void *)e.hS, N, K, group_size,
+                    (const void *)host_S, e.fp != fp ? " and other contents" : "");
+    if (dev_W) *dev_W = static_cast<const int8_t *>(e.dW);
+    if (dev_S) *dev_S = static_cast<const float *>(e.dS);
     return Q3VL_OK;
 }
 
@@ -627,8 +702,7 @@ int q3vl_weight_release(const void *host_W) {
     if (it == g_reg.end())
         return fail(Q3VL_ERR_INVALID_ARGUMENT, "host weight %p is not registered", host_W);
     Q3VL_HIP(hipDeviceSynchronize(), "hipDeviceSynchronize");
-    (void)hipFree(it->second.dW);
-    (void)hipFree(it->second.dS);
+    reg_free(it->second);
     g_reg.erase(it);
     return Q3VL_OK;
 }
@@ -636,10 +710,7 @@ int q3vl_weight_release(const void *host_W) {
 int q3vl_weight_release_all(void) {
     std::lock_guard<std::mutex> lk(g_reg_mu);
     if (!g_reg.empty()) Q3VL_HIP(hipDeviceSynchronize(), "hipDeviceSynchronize");
-    for (auto &kv : g_reg) {
-        (void)hipFree(kv.second.dW);
-        (void)hipFree(kv.second.dS);
-    }
+    for (auto &kv : g_reg) reg_free(kv.second);
     g_reg.clear();
     return Q3VL_OK;
 }

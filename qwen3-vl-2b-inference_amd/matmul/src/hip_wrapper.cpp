@@ -72,11 +72,14 @@ void linear(const void *mat_A, const void *mat_B_in, const void *mat_B_scale,
     if (M == 0 || N == 0) return;
 
     // Weights: device pointers pass through; host weights (mmapped by the
-    // engine's loader) are uploaded once and found again by host address.
+    // engine's loader) are uploaded once and found again by host address,
+    // scale address, shape and a fingerprint of their bytes; a stale entry
+    // (another weight at the same address) is replaced by registering again.
     const int8_t *dW = static_cast<const int8_t *>(mat_B_in);
     const float *dS = static_cast<const float *>(mat_B_scale);
     if (!is_device_ptr(mat_B_in)) {
-        if (q3vl_weight_lookup(mat_B_in, &dW, &dS) != Q3VL_OK &&
+        if (q3vl_weight_lookup(mat_B_in, static_cast<const float *>(mat_B_scale), N, K,
+                               group_size, &dW, &dS) != Q3VL_OK &&
             q3vl_weight_register(static_cast<const int8_t *>(mat_B_in),
                                  static_cast<const float *>(mat_B_scale), N, K, group_size, &dW,
                                  &dS) != Q3VL_OK)

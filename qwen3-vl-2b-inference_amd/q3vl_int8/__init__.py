@@ -54,7 +54,7 @@ def _declare(lib):
         "q3vl_argmax_rows": (i, [_vp, _vp, _sz, _sz, _vp, _sz, _vp]),
         "q3vl_swiglu": (i, [_vp, _vp, _sz, _vp]),
         "q3vl_weight_register": (i, [_vp, _vp, _sz, _sz, _sz, _vp, _vp]),
-        "q3vl_weight_lookup": (i, [_vp, _vp, _vp]),
+        "q3vl_weight_lookup": (i, [_vp, _vp, _sz, _sz, _sz, _vp, _vp]),
         "q3vl_weight_release": (i, [_vp]),
         "q3vl_weight_release_all": (i, []),
         "q3vl_quantize_groupwise": (i, [_vp, _sz, _sz, _vp, _vp, _vp]),

@@ -275,6 +275,7 @@ class Reference:
         L = self.lib
         L.ref_decoder_create.restype = _vp
         L.ref_decoder_create.argtypes = [_vp, _vp, _vp]
+        L.ref_decoder_step.restype = ctypes.c_int
         L.ref_decoder_step.argtypes = [_vp, ctypes.c_int, _sz, _vp]
         L.ref_decoder_destroy.argtypes = [_vp]
         st = _model_struct(dims, arrays)
@@ -282,9 +283,15 @@ class Reference:
         ref = self
 
         class _Dec:
+            max_seq = int(dims["max_seq"])
+
             def step(self_, token, pos):
+                """Logits of forward_text at pos; ValueError (and no call) when
+                pos >= max_seq or the token is outside the vocabulary."""
                 logits = np.zeros(dims["vocab"], np.float32)
-                L.ref_decoder_step(h, int(token), pos, _p(logits))
+                if L.ref_decoder_step(h, int(token), int(pos), _p(logits)) != 0:
+                    raise ValueError(f"reference decode step refused: token {token}, pos {pos}, "
+                                     f"max_seq {dims['max_seq']}, vocab {dims['vocab']}")
                 return logits
 
             def close(self_):

@@ -15,7 +15,7 @@ def test_library_exports_every_declared_function():
     assert len(names) >= 15
     missing = [n for n in names if not hasattr(lib, n)]
     assert not missing, missing
-    assert lib.q3vl_abi_version() == 1
+    assert lib.q3vl_abi_version() == 2
 
 
 def test_linear_dropin_exports_cpp_linear():
@@ -83,3 +83,4 @@ def test_decode_step_rejects_unsupported_models(over, code, text):
                               None)
     assert rc == code, q.last_error()
     assert text in q.last_error()
+

@@ -346,3 +346,59 @@ def test_dropin_linear_host_pointers(orc):
                q.FP32, q.INT8, q.FP32, q.FP32, True, 64)
             assert_bits_equal(C, orc.linear(A, W, S, 64), "drop-in linear")
     q.lib().q3vl_weight_release_all()
+
+
+def _dropin_linear():
+    lib = ctypes.CDLL(q.LINEAR_LIB_PATH)
+    import subprocess
+    sym = [l.split()[-1] for l in subprocess.run(["nm", "-D", q.LINEAR_LIB_PATH], capture_output=True,
+                                                  text=True).stdout.splitlines()
+           if l.split()[-1].startswith("_Z6linear")][0]
+    fn = getattr(lib, sym)
+    vp, sz = ctypes.c_void_p, ctypes.c_size_t
+    fn.argtypes = [vp, vp, vp, vp, vp, vp, sz, sz, sz, ctypes.c_bool, ctypes.c_int, ctypes.c_int,
+                   ctypes.c_int, ctypes.c_int, ctypes.c_bool, sz]
+    return fn
+
+
+def test_registry_reused_host_address(orc):
+    """One host buffer reused for a weight of another shape, then refilled
+    with other values: lookup reports the stale entry, the drop-in linear()
+    re-uploads and matches the oracle each time."""
+    fn = _dropin_linear()
+    L = q.lib()
+    vp = ctypes.c_void_p
+    dW, dS = vp(), vp()
+    buf = np.zeros(2048 * 2048, np.int8)       # one host address for every weight
+    sbuf = np.zeros(2048 * 2048 // 64, np.float32)
+    try:
+        for step, (M, N, K, seed) in enumerate([(1, 2048, 2048, 11), (1, 1024, 2048, 12),
+                                                (3, 2048, 1024, 13), (3, 2048, 1024, 14)]):
+            A, W, S = make_case(seed, M, N, K, 64)
+            Wv = buf[:N * K].reshape(N, K)
+            Sv = sbuf[:N * K // 64].reshape(N, K // 64)
+            Wv[...] = W
+            Sv[...] = S
+            if step:
+                # the previous registration no longer matches this call
+                rc = L.q3vl_weight_lookup(Wv.ctypes.data, Sv.ctypes.data, N, K, 64,
+                                          ctypes.byref(dW), ctypes.byref(dS))
+                assert rc == 5, (step, rc, q.last_error())  # Q3VL_ERR_STALE_WEIGHT
+            C = np.zeros((M, N), np.float32)
+            fn(A.ctypes.data, Wv.ctypes.data, Sv.ctypes.data, None, None, C.ctypes.data, M, N, K,
+               True, q.FP32, q.INT8, q.FP32, q.FP32, True, 64)
+            assert_bits_equal(C, orc.linear(A, W, S, 64), f"drop-in linear after reuse {step}")
+            assert L.q3vl_weight_lookup(Wv.ctypes.data, Sv.ctypes.data, N, K, 64,
+                                        ctypes.byref(dW), ctypes.byref(dS)) == 0
+            got = np.empty_like(W)
+            hip = ctypes.CDLL("libamdhip64.so")
+            hip.hipMemcpy.argtypes = [vp, vp, ctypes.c_size_t, ctypes.c_int]
+            assert hip.hipMemcpy(got.ctypes.data, dW, W.nbytes, 2) == 0  # device to host
+            assert np.array_equal(got, W), f"registered device copy is stale at step {step}"
+        # a wrong scale pointer for a registered weight is stale too
+        assert L.q3vl_weight_lookup(buf.ctypes.data, sbuf.ctypes.data + 64, 2048, 1024, 64,
+                                    ctypes.byref(dW), ctypes.byref(dS)) == 5
+        assert L.q3vl_weight_lookup(buf.ctypes.data + 16, sbuf.ctypes.data, 2048, 1024, 64,
+                                    ctypes.byref(dW), ctypes.byref(dS)) == 1
+    finally:
+        L.q3vl_weight_release_all()
