@@ -182,6 +182,21 @@ int q3vl_decode_step(const q3vl_text_model *m, uint16_t *k_cache, uint16_t *v_ca
                      int32_t *token, int32_t *pos, float *logits, void *workspace,
                      size_t workspace_bytes, q3vl_stream stream);
 
+/* q3vl_decode_step without a workspace argument and without any allocation.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). Its scratch is a static device array of
+ * q3vl_decode_static_scratch_bytes() (1 MiB) per device, held until the
+ * process ends; the first call on a device looks up that device's copy. A
+ * model whose decode scratch (q3vl_decode_workspace_bytes) exceeds it is
+ * refused with Q3VL_ERR_UNSUPPORTED before any device work. Every call on a
+ * device shares the one array, so calls that overlap on one device (other
+ * streams, other threads) race; the scratch holds no state between calls.
+ * Same kernels and results as q3vl_decode_step. */
+int q3vl_decode_step_static(const q3vl_text_model *m, uint16_t *k_cache, uint16_t *v_cache,
+                            int32_t *token, int32_t *pos, float *logits, q3vl_stream stream);
+size_t q3vl_decode_static_scratch_bytes(void);
+
 /* ---- checkpoint files: the reference's single-file .bin
  * (model/src/load_model.cpp:50-246, written by
  * export_bin/export_qwen_bin.py:212-420). A 100-byte header

@@ -372,6 +372,37 @@ int check_model(const q3vl_text_model *m) {
 int decode_step_on(const q3vl_text_model *m, uint16_t *k_cache, uint16_t *v_cache,
                    int32_t *token, int32_t *pos, float *logits, char *w, hipStream_t st);
 
+// ---- static scratch of q3vl_decode_step_static (no allocation per call).
+// The array's host-side name is not a device address: each device's copy is
+// found once with hipGetSymbolAddress (with that device current) and that
+// pointer is what the kernels receive.
+constexpr size_t kStaticScratchBytes = (size_t)1 << 20;  // 1 MiB per device
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices] = {};
+
+}  // namespace
+
+static __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
+
+namespace {
+
+int static_scratch(char **out) {
+    int dev = 0;
+    Q3VL_HIP(hipGetDevice(&dev), "hipGetDevice");
+    if (dev < 0 || dev >= kMaxDevices) return fail(Q3VL_ERR_UNSUPPORTED, "device %d", dev);
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void *p = nullptr;
+        Q3VL_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+        if (!p || ((uintptr_t)p & 255u))
+            return fail(Q3VL_ERR_HIP, "static scratch at %p is not 256-byte aligned", p);
+        g_scratch_ptr[dev] = p;
+    }
+    *out = static_cast<char *>(g_scratch_ptr[dev]);
+    return Q3VL_OK;
+}
+
 GemvArgs gemv1(const float *A, int K, int gs) {
     GemvArgs a{};
     a.A = A;
@@ -528,6 +559,26 @@ int q3vl_decode_step(const q3vl_text_model *m, uint16_t *k_cache, uint16_t *v_ca
     const DecodeLayout L = decode_layout(m);
     char *w = nullptr;
     rc = resolve_ws(workspace, workspace_bytes, L.total, &w);
+    if (rc) return rc;
+    return decode_step_on(m, k_cache, v_cache, token, pos, logits, w, (hipStream_t)stream);
+}
+
+size_t q3vl_decode_static_scratch_bytes(void) { return kStaticScratchBytes; }
+
+int q3vl_decode_step_static(const q3vl_text_model *m, uint16_t *k_cache, uint16_t *v_cache,
+                            int32_t *token, int32_t *pos, float *logits, q3vl_stream stream) {
+    int rc = check_model(m);
+    if (rc) return rc;
+    if (!k_cache || !v_cache || !token || !pos)
+        return fail(Q3VL_ERR_INVALID_ARGUMENT, "null cache / token / pos");
+    const size_t need = decode_layout(m).total;
+    if (need > kStaticScratchBytes)
+        return fail(Q3VL_ERR_UNSUPPORTED,
+                    "decode step needs %zu bytes of scratch, more than the %zu of the static "
+                    "scratch (use q3vl_decode_step with a caller workspace)",
+                    need, kStaticScratchBytes);
+    char *w = nullptr;
+    rc = static_scratch(&w);
     if (rc) return rc;
     return decode_step_on(m, k_cache, v_cache, token, pos, logits, w, (hipStream_t)stream);
 }

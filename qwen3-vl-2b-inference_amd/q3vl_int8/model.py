@@ -77,6 +77,25 @@ def decode_step(model: DeviceTextModel, k_cache, v_cache, token, pos, logits=Non
                               _ptr(pos), _ptr(logits), wp, wb, _stream(stream)))
 
 
+def decode_step_static(model: DeviceTextModel, k_cache, v_cache, token, pos, logits=None,
+                       stream=None):
+    """decode_step with the library's static device scratch instead of a
+    workspace: allocates nothing. Calls that overlap on one device race."""
+    from . import _check, _ptr, _stream, lib
+    L = lib()
+    L.q3vl_decode_step_static.restype = ctypes.c_int
+    L.q3vl_decode_step_static.argtypes = [ctypes.POINTER(TextModelC), _vp, _vp, _vp, _vp, _vp, _vp]
+    _check(L.q3vl_decode_step_static(ctypes.byref(model.c), _ptr(k_cache), _ptr(v_cache),
+                                     _ptr(token), _ptr(pos), _ptr(logits), _stream(stream)))
+
+
+def static_scratch_bytes() -> int:
+    from . import lib
+    L = lib()
+    L.q3vl_decode_static_scratch_bytes.restype = ctypes.c_size_t
+    return L.q3vl_decode_static_scratch_bytes()
+
+
 def alloc_decode_workspace(model: DeviceTextModel, device="cuda"):
     """Zero-filled device workspace sized for decode_step on this model."""
     import torch

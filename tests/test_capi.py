@@ -84,3 +84,22 @@ def test_decode_step_rejects_unsupported_models(over, code, text):
     assert rc == code, q.last_error()
     assert text in q.last_error()
 
+
+def test_static_decode_rejects_oversized_scratch():
+    """q3vl_decode_step_static refuses a model whose decode scratch exceeds
+    its static array, before any device work (so it runs without a GPU)."""
+    from q3vl_int8 import model as qm
+    L = q.lib()
+    L.q3vl_decode_static_scratch_bytes.restype = ctypes.c_size_t
+    cap = L.q3vl_decode_static_scratch_bytes()
+    assert cap == 1 << 20
+    dims = dict(vocab=151936, hidden=8192, inter=8192, layers=1, heads=64, kv_heads=64,
+                head_dim=128, max_seq=4096, gs=64, eps=1e-6)
+    fake = 1 << 20  # non-null, aligned, never dereferenced
+    c = qm.make_struct(dims, lambda n: fake)
+    assert qm.decode_workspace_bytes(type("M", (), {"c": c})()) > cap
+    L.q3vl_decode_step_static.restype = ctypes.c_int
+    L.q3vl_decode_step_static.argtypes = [ctypes.POINTER(qm.TextModelC)] + [ctypes.c_void_p] * 6
+    rc = L.q3vl_decode_step_static(ctypes.byref(c), fake, fake, fake, fake, fake, None)
+    assert rc == q.ERR_UNSUPPORTED
+    assert "static scratch" in q.last_error()
