@@ -895,9 +895,8 @@ def main():
         results.extend(out)
         torch.cuda.empty_cache()
     by = {r["name"]: r for r in results}
-    head = by.get("cfg1_decode_step")
-    if head is None:
-        raise SystemExit("the headline needs cfg1 in --configs")
+    head = by.get("cfg1_decode_step") or dict(name="cfg1_decode_step",
+                                              error="cfg1 (the headline) not in --configs")
 
     cpu = None
     if cpu_res is not None:

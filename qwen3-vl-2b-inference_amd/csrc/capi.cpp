@@ -75,12 +75,16 @@ WsLayout layout(size_t M, size_t N, size_t K, size_t gs) {
     L.parts_idx = off;
     off += align256(kMaxGemvParts * mm * sizeof(int32_t));
     if (M > 8) {
+        // rows padded to whole 32-row m-tiles (the fragment-order layout of
+        // the group-64 GEMM; the transposed scales of the others use the same
+        // stride)
         const size_t Kg = gs ? K / gs : 0;
-        L.lda_s = (int)((M + 3) & ~(size_t)3);
+        const size_t Mpad = (M + 31) & ~(size_t)31;
+        L.lda_s = (int)Mpad;
         L.aq = off;
-        off += align256(M * K * 2);
+        off += align256(Mpad * K * 2);
         L.as = off;
-        off += align256(Kg * (size_t)L.lda_s * 4);
+        off += align256(Kg * Mpad * 4);
         L.logits = off;
         off += align256(M * N * 4);
     }
@@ -129,6 +133,26 @@ int resolve_ws(void *user, size_t user_bytes, size_t need, char **out) {
         g_ws.size[dev] = sz;
     }
     *out = static_cast<char *>(g_ws.buf[dev]);
+    return Q3VL_OK;
+}
+
+// Compute units of the current device (cached per device).
+int device_cus(int *cus) {
+    static std::atomic<int> cache[64];
+    int dev = 0;
+    Q3VL_HIP(hipGetDevice(&dev), "hipGetDevice");
+    if (dev >= 0 && dev < 64) {
+        const int c = cache[dev].load(std::memory_order_relaxed);
+        if (c > 0) {
+            *cus = c;
+            return Q3VL_OK;
+        }
+    }
+    int c = 0;
+    Q3VL_HIP(hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev), "CU count");
+    if (c < 1) c = 1;
+    if (dev >= 0 && dev < 64) cache[dev].store(c, std::memory_order_relaxed);
+    *cus = c;
     return Q3VL_OK;
 }
 
@@ -220,6 +244,42 @@ int run_linear(const float *A, int nseg, const int8_t *const *W, const float *co
     }
     _Float16 *aq = reinterpret_cast<_Float16 *>(wbase + LG.aq);
     float *asT = reinterpret_cast<float *>(wbase + LG.as);
+    // Group size 64 without group sums: the fragment-order GEMM where it
+    // serves every segment's shape (it addresses its buffers with 32-bit byte
+    // offsets), with the activations quantized into MFMA fragment order; one
+    // GEMM per segment, gate and up together under SwiGLU.
+    bool use_mf = gs == 64 && ((M + 31) & ~(size_t)31) * K * 2 <= 0x7fffffffULL &&
+                  (size_t)Ns[0] * K <= 0x7fffffffULL;
+    int cus = 0;
+    if (use_mf) {
+        rc = device_cus(&cus);
+        if (rc) return rc;
+    }
+    for (int i = 0; use_mf && i < nseg; ++i)
+        use_mf = !(G && G[i]) && (size_t)Ns[i] * K <= 0x7fffffffULL &&
+                 gemm_mf_serves((int)M, (int)Ns[i], (int)K, mode == GEMV_SWIGLU, cus);
+    if (use_mf) {
+        Q3VL_HIP(launch_quantize_frag(A, aq, asT, (int)M, (int)K, st), "quantize launch");
+        const int Mt = (int)((M + 31) / 32);
+        if (mode == GEMV_SWIGLU) {
+            GemmMfArgs g{aq, asT, Mt, W[0], S[0], W[1], S[1], C[0], (int)M, (int)Ns[0], (int)K};
+            Q3VL_HIP(launch_gemm_mf(g, true, cus, st), "gemm launch");
+            return Q3VL_OK;
+        }
+        for (int i = 0; i < nseg; ++i) {
+            float *Ci = C[i];
+            if (mode == GEMV_ARGMAX && !Ci) Ci = reinterpret_cast<float *>(wbase + LG.logits);
+            GemmMfArgs g{aq, asT, Mt, W[i], S[i], nullptr, nullptr, Ci, (int)M, (int)Ns[i], (int)K};
+            Q3VL_HIP(launch_gemm_mf(g, false, cus, st), "gemm launch");
+            if (mode == GEMV_ARGMAX)
+                Q3VL_HIP(launch_argmax_rows(Ci, (int)M, (int)Ns[i],
+                                            reinterpret_cast<float *>(wbase + LG.parts_val),
+                                            reinterpret_cast<int32_t *>(wbase + LG.parts_idx),
+                                            kGemmArgmaxParts, ids, st),
+                         "argmax launch");
+        }
+        return Q3VL_OK;
+    }
     Q3VL_HIP(launch_quantize_f16(A, aq, asT, (int)M, (int)K, (int)gs, (int)K, LG.lda_s, st),
              "quantize launch");
     if (mode == GEMV_SWIGLU) {

@@ -1,0 +1,412 @@
+// gemm_mf.hip -- int8-weight GEMM for M > 8 at group size 64 (gfx950), with
+// activations in MFMA fragment order.
+//
+// Reference: the general path of linear_int8_fp32s_int32acc_transpose,
+// matmul/src/cpu_f32a_i8f32sb_f32c_avx2.cpp:477-662: for each output and
+// each K-group g in ascending order, G = sum_{k in g} q[m,k] * w[n,k] exactly
+// (int32), then acc = fma(float(G) * a_s[m,g], w_s[n,g], acc) (:613-617,
+// 652; GCC contracts the multiply-add, which the golden vectors pin).
+//
+// Exactness. q (int16, |q| <= 1016) and w (int8) are exact in fp16, and every
+// partial sum of one group is an integer below 2^24, so
+// v_mfma_f32_32x32x16_f16 over the group's 64 k with a zero initial
+// accumulator yields G exactly. The fp32 epilogue consumes it group by group.
+//
+// Data movement, from what this hardware measured (per CU: LDS reads about
+// 110 B/clk, L1 about 62 B/clk, one 32x32x16 MFMA about 34 cycles; the
+// epilogue's two fp32 operations per output and group cost as much VALU time
+// as the MFMAs, so the kernel is VALU-bound and the operand traffic is split
+// between the two paths):
+// * A: the quantizer writes q in fragment order -- per 32-row m-tile t and
+//   group g a 4 KB chunk [slice s][lane l][8 halves] holding
+//   q[32t + l%32][64g + 32(l/32) + 8s + j] -- so each wave loads its A
+//   fragments straight from L1/L2 with one coalesced 1 KB read per slice.
+//   Its scales come in the same order: [t][g][l/32][16] holds a_s of rows
+//   32t + 8(e/4) + 4(l/32) + e%4, the rows a lane's 16 accumulators hold.
+// * B: the block loads its weight rows (64 bytes per row and group) once,
+//   widens them to fp16 (0x64xx exponent trick) and stores them in LDS in the
+//   same fragment order, two buffers deep, so every wave reads its B
+//   fragments with one ds_read_b128 per slice and n-tile. The 16-byte slots
+//   are swizzled (slot ^ 4*(s/2) ^ 8*(l/32)) so that the writers' and the
+//   readers' 16-lane passes each hit 16 distinct bank groups.
+// * The k order inside a group: slice s of lane half h covers k = 32h + 8s +
+//   j; A and B use the same map, so each MFMA pairs matching k and the four
+//   slices cover the group's 64 k once.
+// * Block: 4 waves in 2 x 2, wave tile (32 TM) x (32 TN); two or three
+//   blocks share a CU, so one block's epilogue overlaps another's MFMAs and
+//   its loads another's waits. One barrier per group (an LDS-only fence).
+//   SWIGLU: the block's B rows are 32 TN gate rows and the same up rows; wave
+//   wn holds gate n-tile wn and up n-tile 2 + wn, so silu(gate) * up needs no
+//   exchange.
+#include "q3vl_device.hpp"
+#include "q3vl_kernels.hpp"
+
+namespace q3vl {
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef float float16_t __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------- fragment-order quantizer
+// The reference quantizer (cpu_f32a_i8f32sb_f32c_avx2.cpp:135-177), as
+// quantize_rows_kernel computes it (16 lanes per group: lane i runs the FMA
+// chain over x[16t + i], then the fixed tree), writing q as fp16 in the
+// fragment order above and a_s in its fragment order. Rows M .. 32*Mt-1 are
+// written as zeros. One row and 16 groups per 256-thread block.
+__global__ __launch_bounds__(256) void quantize_frag_kernel(const float *__restrict__ A,
+                                                            _Float16 *__restrict__ qf,
+                                                            float *__restrict__ asf, int M, int K) {
+    const int Kg = K / 64;
+    const int lane16 = threadIdx.x & 15;
+    const int g = blockIdx.x * 16 + (threadIdx.x >> 4);
+    const int m = blockIdx.y;
+    if (g >= Kg) return;  // whole 16-lane groups leave together
+    const bool real = m < M;
+    const float *x = A + (size_t)(real ? m : 0) * K + (size_t)g * 64;
+    float v[4];
+    float p = 0.0f;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        v[t] = x[16 * t + lane16];
+        p = fmaf(v[t], v[t], p);
+    }
+    p = p + __shfl_xor(p, 8, 16);
+    p = p + __shfl_xor(p, 4, 16);
+    p = p + __shfl_xor(p, 1, 16);
+    p = p + __shfl_xor(p, 2, 16);
+    const float s = group_scale(p, 1.0f / 64.0f);
+    const float inv = rcp_rn(s);
+    const int mt = m >> 5, r = m & 31;
+    const size_t chunk0 = ((size_t)mt * Kg + g) * 4;  // 16-byte chunk index of slice 0, lane 0
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        const int k = 16 * t + lane16;               // k inside the group
+        const int h = k >> 5, sl = (k >> 3) & 3, j = k & 7;
+        const float qv = real ? (float)quant_cvt(v[t] * inv) : 0.0f;
+        qf[((chunk0 + sl) * 64 + r + 32 * h) * 8 + j] = (_Float16)qv;
+    }
+    if (lane16 == 0) {
+        const int h = (r >> 2) & 1, e = 4 * (r >> 3) + (r & 3);
+        asf[(((size_t)mt * Kg + g) * 2 + h) * 16 + e] = real ? s : 0.0f;
+    }
+}
+
+hipError_t launch_quantize_frag(const float *A, _Float16 *qf, float *asf, int M, int K,
+                                hipStream_t st) {
+    if (K % 64 != 0 || M < 1) return hipErrorInvalidValue;
+    const int Mt = (M + 31) / 32;
+    dim3 grid((K / 64 + 15) / 16, Mt * 32);
+    quantize_frag_kernel<<<grid, 256, 0, st>>>(A, qf, asf, M, K);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------- the GEMM
+// 4 bytes (already xor 0x80) -> 4 fp16 values in two dwords:
+// half(0x6400 | b') - 1152 = b' - 128 = b.
+__device__ __forceinline__ void widen4_mf(uint32_t x, uint32_t &lo, uint32_t &hi) {
+    const uint32_t e = 0x64646464u;
+    const uint32_t l = __builtin_amdgcn_perm(e, x, 0x04010400u);
+    const uint32_t hh = __builtin_amdgcn_perm(e, x, 0x04030402u);
+    const half2_t off = {(_Float16)1152.0f, (_Float16)1152.0f};
+    lo = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, l) - off);
+    hi = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, hh) - off);
+}
+
+// Swizzled 16-byte slot of (slice s, lane l) inside an n-tile's 4 KB.
+__device__ __forceinline__ int bslot(int s, int l) {
+    return s * 64 + (l ^ ((s & 2) << 1) ^ ((l & 32) >> 2));
+}
+
+// BPC: blocks per CU the register budget is sized for. D: groups whose global
+// loads are in flight (a ring of D register sets). Loads return in order, so
+// every operand of a group -- A fragments, raw B, a_s, w_s -- is issued at the
+// same distance D ahead. A ring value is consumed (A by the MFMAs, the rest
+// by the staging into LDS) before its slot is reloaded; a value copied out of
+// the ring into other registers would make each reload wait for that copy's
+// load, which the in-order return turns into a wait for the whole ring.
+template <int TM, int TN, bool SWIGLU, int D, int BPC>
+__global__ __launch_bounds__(256, BPC) void gemm_mf_kernel(GemmMfArgs a) {
+    constexpr int BM = 64 * TM;             // rows of the block
+    constexpr int BN = 64 * TN;             // weight rows of the block
+    constexpr int NT = BN / 32;             // n-tiles in the B buffer
+    constexpr int BCH = BN * 4 / 256;       // 16-byte weight chunks per thread and group
+    constexpr int BBUF = NT * 4 * 64 * 16;  // bytes of one B buffer
+    static_assert(!SWIGLU || TN == 2, "SwiGLU pairs one gate and one up n-tile per wave");
+    extern __shared__ __align__(16) unsigned char smem[];
+    float *asl = reinterpret_cast<float *>(smem + 2 * BBUF);  // [3][2TM m-tiles][32]
+    float *wsl = asl + 3 * 64 * TM;                             // [3][BN]
+
+    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    const int wm = wid & 1, wn = wid >> 1;
+    const int M = a.M, N = a.N, K = a.K, Kg = K / 64, Mt = a.Mt;
+    const int ncols = SWIGLU ? BN / 2 : BN;  // output columns of the block
+    // XCD-aware tile order. Workgroups go to the 8 XCDs round-robin (block b
+    // to XCD b % 8), and each XCD has its own L2. Tile t = xcd * per + b / 8
+    // gives XCD x the contiguous tiles [x per, (x+1) per), taken M-tile
+    // fastest: a few columns of weight rows (which then stay in that XCD's
+    // L2) against all activation rows, read by the XCD's blocks in step.
+    const int tiles_m = (Mt + 2 * TM - 1) / (2 * TM);
+    const int tiles = tiles_m * ((N + ncols - 1) / ncols);
+    const int per = (tiles + 7) / 8;
+    const int t = (int)(blockIdx.x % 8) * per + (int)(blockIdx.x / 8);
+    if (t >= tiles) return;  // whole block: before any barrier
+    const int n0 = (t / tiles_m) * ncols;
+    const int mt0 = (t % tiles_m) * 2 * TM;  // first m-tile of the block
+
+    // Global loads go through buffer resources (SGPR base and size, 32-bit
+    // per-lane offsets, the per-group advance in the scalar offset); a read
+    // past a buffer's size returns zeros.
+    constexpr int kRsrcWord3 = 0x00020000;
+    const __amdgpu_buffer_rsrc_t rA =
+        __builtin_amdgcn_make_buffer_rsrc((void *)a.Af, 0, Mt * Kg * 4096, kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t rAS =
+        __builtin_amdgcn_make_buffer_rsrc((void *)a.asf, 0, Mt * Kg * 128, kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t rW0 =
+        __builtin_amdgcn_make_buffer_rsrc((void *)a.W0, 0, N * K, kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t rW1 =
+        __builtin_amdgcn_make_buffer_rsrc((void *)(SWIGLU ? a.W1 : a.W0), 0, N * K, kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t rS0 =
+        __builtin_amdgcn_make_buffer_rsrc((void *)a.S0, 0, N * Kg * 4, kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t rS1 =
+        __builtin_amdgcn_make_buffer_rsrc((void *)(SWIGLU ? a.S1 : a.S0), 0, N * Kg * 4, kRsrcWord3);
+
+    // ---- A fragment offsets of this wave (m-tiles clamped into the buffer)
+    int aoff[TM];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+        const int mt = min(mt0 + wm * TM + i, Mt - 1);
+        aoff[i] = (mt * Kg * 256 + lane) * 16;
+    }
+    // ---- B staging: chunk q = tid + 256 i -> row q / 4, 16-byte piece q % 4
+    // (under SWIGLU the chunks with i >= BCH / 2 are the up rows)
+    int boff[BCH];
+    int bdst0[BCH], bdst1[BCH];
+#pragma unroll
+    for (int i = 0; i < BCH; ++i) {
+        const int q = tid + 256 * i;
+        const int row = q >> 2, c = q & 3;
+        const int nrow = min(n0 + (SWIGLU && row >= BN / 2 ? row - BN / 2 : row), N - 1);
+        boff[i] = nrow * K + 16 * c;
+        const int nt = row >> 5, l = (row & 31) + 32 * (c >> 1), s0 = 2 * (c & 1);
+        bdst0[i] = (nt * 256 + bslot(s0, l)) * 16;
+        bdst1[i] = (nt * 256 + bslot(s0 + 1, l)) * 16;
+    }
+    // ---- a_s staging: threads < 16 TM copy one float4 each (2 TM m-tiles of
+    // 32 scales per group)
+    int as_off = 0, as_dst = 0;
+    const bool as_thr = tid < 16 * TM;
+    if (as_thr) {
+        const int i = tid >> 3, part = tid & 7;  // m-tile i of the block, 16 B piece
+        const int mt = min(mt0 + i, Mt - 1);
+        as_off = (mt * Kg * 32 + 4 * part) * 4;
+        as_dst = i * 32 + 4 * part;
+    }
+    // ---- w_s staging: thread t < BN copies the scale of B row t each group
+    const bool ws_thr = tid < BN;
+    const bool ws_up = SWIGLU && tid >= BN / 2;
+    const int ws_off = min(n0 + (ws_up ? tid - BN / 2 : (ws_thr ? tid : 0)), N - 1) * Kg * 4;
+    // ---- this lane's output columns (n-tile bt[j] of the B buffer)
+    int bt[TN];
+    int ncol[TN];
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+        if (SWIGLU) {
+            bt[j] = j == 0 ? wn : 2 + wn;
+            ncol[j] = n0 + 32 * wn + (lane & 31);
+        } else {
+            bt[j] = TN * wn + j;
+            ncol[j] = n0 + 32 * (TN * wn + j) + (lane & 31);
+        }
+    }
+    const int h = lane >> 5;
+
+    // ---- the ring of in-flight loads: group g's operands in slot g % D
+    u32x4 braw[D][BCH];
+    float4 asraw[D];
+    u32x4 af[D][TM][4];
+    float wsraw[D];
+    auto load_group = [&](int sl, int g) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+                af[sl][i][s] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                             rA, aoff[i], g * 4096 + s * 1024, 0));
+#pragma unroll
+        for (int i = 0; i < BCH; ++i) {
+            const bool up = SWIGLU && i >= BCH / 2;
+            braw[sl][i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                        up ? rW1 : rW0, boff[i], 64 * g, 0));
+        }
+        // (threads past the 2 TM m-tiles read scales at offset 128 g of the
+        // buffer and discard them: the scalar offset stays uniform)
+        asraw[sl] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rAS, as_off, 128 * g, 0));
+        wsraw[sl] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                  ws_up ? rS1 : rS0, ws_off, 4 * g, 0));
+    };
+    // group g's B (ring slot sl) goes to B buffer g % 2, its scales to the
+    // a_s and w_s slots g % 3 (every ring value is consumed here, before its
+    // slot is reloaded, so a reload never waits for the load it replaces)
+    auto stage = [&](int sl, int g) {
+        unsigned char *Bs = smem + (g & 1) * BBUF;
+#pragma unroll
+        for (int i = 0; i < BCH; ++i) {
+            const u32x4 v = braw[sl][i] ^ (u32x4){0x80808080u, 0x80808080u, 0x80808080u, 0x80808080u};
+            uint32_t w[8];
+            widen4_mf(v.x, w[0], w[1]);
+            widen4_mf(v.y, w[2], w[3]);
+            widen4_mf(v.z, w[4], w[5]);
+            widen4_mf(v.w, w[6], w[7]);
+            *reinterpret_cast<u32x4 *>(Bs + bdst0[i]) = (u32x4){w[0], w[1], w[2], w[3]};
+            *reinterpret_cast<u32x4 *>(Bs + bdst1[i]) = (u32x4){w[4], w[5], w[6], w[7]};
+        }
+        if (as_thr) *reinterpret_cast<float4 *>(asl + (g % 3) * 64 * TM + as_dst) = asraw[sl];
+        if (ws_thr) wsl[(g % 3) * BN + tid] = wsraw[sl];
+    };
+
+    // one accumulator set: the MFMA -> epilogue chain of one wave is hidden
+    // by the other blocks on the CU
+    float16_t acc[TM][TN], out[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) out[i][j] = (float16_t)(0.0f);
+
+    // ---- prologue: groups 0 .. D-1 in flight (clamped: a repeated load of
+    // the last group keeps the ring full), group 0 staged
+#pragma unroll
+    for (int j = 0; j < D; ++j) load_group(j, min(j, Kg - 1));
+    stage(0, 0);
+    __syncthreads();
+
+    // B fragments of group g (all four slices, issued together)
+    auto read_b = [&](half8_t (&bfr)[4][TN], int g) {
+        const unsigned char *Bs = smem + (g & 1) * BBUF;
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+                bfr[s][j] = *reinterpret_cast<const half8_t *>(Bs + (bt[j] * 256 + bslot(s, lane)) * 16);
+    };
+    auto mfmas = [&](int sl, const half8_t (&bfr)[4][TN]) {
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                        __builtin_bit_cast(half8_t, af[sl][i][s]), bfr[s][j],
+                        s == 0 ? (float16_t)(0.0f) : acc[i][j], 0, 0, 0);
+    };
+    // epilogue of group g, reference order: out = fma(G * a_s, w_s, out)
+    auto epilogue = [&](int g) {
+        const float *as_g = asl + (g % 3) * 64 * TM + wm * TM * 32 + h * 16;
+        float ws_g[TN];
+#pragma unroll
+        for (int j = 0; j < TN; ++j) ws_g[j] = wsl[(g % 3) * BN + bt[j] * 32 + (lane & 31)];
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+            float asv[16];
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4) {
+                const float4 v = *reinterpret_cast<const float4 *>(as_g + i * 32 + 4 * q4);
+                asv[4 * q4] = v.x;
+                asv[4 * q4 + 1] = v.y;
+                asv[4 * q4 + 2] = v.z;
+                asv[4 * q4 + 3] = v.w;
+            }
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+#pragma unroll
+                for (int e = 0; e < 16; ++e)
+                    out[i][j][e] = fmaf(acc[i][j][e] * asv[e], ws_g[j], out[i][j][e]);
+        }
+    };
+    // group g (ring slot sl = g % D): MFMAs from B buffer g % 2, reload slot
+    // sl with group g+D, stage group g+1, the epilogue, barrier
+    auto group = [&](int sl, int g) {
+        half8_t bfr[4][TN];
+        read_b(bfr, g);
+        mfmas(sl, bfr);
+        // slot sl's A went into the MFMAs above and its B was staged one
+        // group ago, so it takes group g+D now; issued before the staging of
+        // group g+1 (slot (g+1) % D, which is slot sl itself when D = 1).
+        // Unconditional (the last group is reloaded near the end), so the
+        // compiler's count of loads in flight is the same on every path.
+        load_group(sl, min(g + D, Kg - 1));
+        if (g + 1 < Kg) stage((sl + 1) % D, g + 1);
+        epilogue(g);
+        // LDS-only barrier: a __syncthreads() here would also wait for every
+        // global load in flight and empty the load ring at each group
+        lds_barrier();
+    };
+    for (int g0 = 0; g0 < Kg; g0 += D) {  // unrolled by D: ring slots static
+#pragma unroll
+        for (int j = 0; j < D; ++j)
+            if (g0 + j < Kg) group(j, g0 + j);  // uniform
+    }
+
+    // ---- store
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+        const int rbase = 32 * (mt0 + wm * TM + i) + 4 * h;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const int mrow = rbase + 8 * (e >> 2) + (e & 3);
+            if (mrow >= M) continue;
+            if constexpr (SWIGLU) {
+                if (ncol[0] < N) a.C[(size_t)mrow * N + ncol[0]] = silu_mul(out[i][0][e], out[i][1][e]);
+            } else {
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+                    if (ncol[j] < N) a.C[(size_t)mrow * N + ncol[j]] = out[i][j][e];
+            }
+        }
+    }
+}
+
+template <int TM, int TN, bool SWIGLU, int D, int BPC>
+static hipError_t launch_mf(const GemmMfArgs &a, hipStream_t st) {
+    constexpr int BN = 64 * TN;
+    const int ncols = SWIGLU ? BN / 2 : BN;
+    const int tiles = ((a.N + ncols - 1) / ncols) * ((a.Mt + 2 * TM - 1) / (2 * TM));
+    const int grid = 8 * ((tiles + 7) / 8);  // see the tile order in the kernel
+    const size_t lds = 2 * (BN / 32) * 4 * 64 * 16 + 3 * 64 * TM * 4 + 3 * BN * 4;
+    gemm_mf_kernel<TM, TN, SWIGLU, D, BPC><<<grid, 256, lds, st>>>(a);
+    return hipGetLastError();
+}
+
+// Where this kernel serves (the caller quantizes in fragment order for it)
+// and with which tiles, from timings of the prefill and vision shapes on
+// MI355X. SwiGLU: always; 64 x (64 gate + 64 up) tiles at 3 blocks per CU
+// while the grid fits one round of the device, else 128-row tiles. Plain:
+// while 64 x 64 tiles give every CU at least two blocks; 128 x 64 tiles once
+// those give every CU about two. Long-K shapes with fewer tiles (down_proj at
+// M = 512, the vision fc2 and merger at K = 4096) run faster on
+// gemm_g64_kernel, whose A tiles go through LDS.
+static long mf_blocks(const GemmMfArgs &a, int tm, int ncols) {
+    return (long)((a.N + ncols - 1) / ncols) * ((a.Mt + 2 * tm - 1) / (2 * tm));
+}
+
+bool gemm_mf_serves(int M, int N, int K, bool swiglu, int cus) {
+    if (K % 64 != 0 || K < 64 || M < 1 || N < 1) return false;
+    if (swiglu) return true;
+    GemmMfArgs a{};
+    a.Mt = (M + 31) / 32;
+    a.N = N;
+    return mf_blocks(a, 1, 64) >= 2L * cus;
+}
+
+hipError_t launch_gemm_mf(const GemmMfArgs &a, bool swiglu, int cus, hipStream_t st) {
+    if (a.K % 64 != 0 || a.K < 64 || a.M < 1 || a.N < 1) return hipErrorInvalidValue;
+    if (swiglu) {
+        if (mf_blocks(a, 1, 64) <= 3L * cus) return launch_mf<1, 2, true, 1, 3>(a, st);
+        return launch_mf<2, 2, true, 1, 2>(a, st);
+    }
+    if (4 * mf_blocks(a, 2, 64) >= 7L * cus) return launch_mf<2, 1, false, 2, 2>(a, st);
+    return launch_mf<1, 1, false, 2, 2>(a, st);
+}
+
+}  // namespace q3vl

@@ -114,4 +114,25 @@ struct GemmArgs {
 };
 hipError_t launch_gemm(const GemmArgs &a, hipStream_t st);
 
+// Group size 64: activations quantized into MFMA fragment order
+// (launch_quantize_frag), then the fragment-order GEMM.
+struct GemmMfArgs {
+    const _Float16 *Af;  // [Mt][K/64][4][64][8] fp16 fragments of q (Mt = ceil(M/32))
+    const float *asf;    // [Mt][K/64][2][16] activation scales in accumulator order
+    int Mt;
+    const int8_t *W0;    // [N, K] (gate when swiglu)
+    const float *S0;     // [N, K/64]
+    const int8_t *W1;    // up weights when swiglu, else null
+    const float *S1;
+    float *C;            // [M, N] (H when swiglu)
+    int M, N, K;
+};
+// qf must hold 32*ceil(M/32)*K halves, asf 32*ceil(M/32)*K/64 floats.
+hipError_t launch_quantize_frag(const float *A, _Float16 *qf, float *asf, int M, int K,
+                                hipStream_t st);
+// Whether the fragment-order GEMM serves an M x N x K product (else
+// launch_gemm's kernels, with launch_quantize_f16), on a device of `cus` CUs.
+bool gemm_mf_serves(int M, int N, int K, bool swiglu, int cus);
+hipError_t launch_gemm_mf(const GemmMfArgs &a, bool swiglu, int cus, hipStream_t st);
+
 }  // namespace q3vl

@@ -122,14 +122,16 @@ def test_gemm_parity(orc, M, N, K, gs):
 
 @pytest.mark.parametrize("M,N,K", [(9, 128, 1024), (100, 200, 2048), (130, 260, 1024),
                                    (784, 3072, 1024), (196, 2048, 4096), (512, 8192, 1024),
-                                   (513, 8200, 1024)])
+                                   (513, 8200, 1024), (512, 2048, 6144), (1030, 8200, 128),
+                                   (1024, 8192, 256)])
 def test_gemm_group64_tiles_parity(orc, M, N, K):
-    """The group-64 MFMA GEMM at each of its tile shapes (64x64, 64x128,
-    128x128 chosen by grid size), ragged M and N, bit-exact."""
+    """The group-64 MFMA GEMM at each of its tile variants (64x64 tiles with
+    a deep load ring at one block per CU or a short ring at several, 128x128
+    tiles once the grid gives every CU two), ragged M and N, bit-exact."""
     run_linear_case(orc, M, N, K, 64, seed=7 * M + N + K, groups=False)
 
 
-@pytest.mark.parametrize("M,N,K", [(100, 200, 1024), (333, 1030, 2048)])
+@pytest.mark.parametrize("M,N,K", [(100, 200, 1024), (333, 1030, 2048), (1030, 6200, 128)])
 def test_gemm_swiglu_ragged_parity(orc, M, N, K):
     A, Wg, Sg = make_case(900 + M, M, N, K, 64)
     _, Wu, Su = make_case(901 + M, M, N, K, 64)
@@ -198,7 +200,7 @@ def test_extreme_activation_groups(orc, M):
 
 # -------------------------------------------------------------- fused consumers
 @pytest.mark.parametrize("M,N,K", [(1, 6144, 2048), (1, 1024, 1024), (4, 512, 1024), (64, 512, 1024),
-                                   (512, 768, 2048)])
+                                   (512, 768, 2048), (512, 6144, 2048), (300, 8200, 1024)])
 def test_swiglu_fused_parity(orc, M, N, K):
     gs = 64
     A, Wg, Sg = make_case(100 + M, M, N, K, gs)
@@ -258,11 +260,23 @@ def test_lm_head_argmax_parity(orc, M):
     np.testing.assert_array_equal(ids2, ids_ref)
 
 
-def test_lm_head_argmax_gemm_path(orc):
-    M, V, K, gs = 12, 5000, 1024, 64
-    A, W, S = make_case(77, M, V, K, gs)
-    ids = host(q.lm_head_argmax(dev(A), dev(W), dev(S), gs))
-    np.testing.assert_array_equal(ids, orc.argmax_rows(orc.linear(A, W, S, gs)))
+@pytest.mark.parametrize("M,V,K", [(12, 5000, 1024), (40, 33000, 2048)])
+def test_lm_head_argmax_gemm_path(orc, M, V, K):
+    """lm_head + argmax for M > 8 (the GEMM, then the row argmax), with a
+    planted tie that the lowest index must win, logits bit-exact."""
+    gs = 64
+    A, W, S = make_case(77 + M, M, V, K, gs)
+    top = int(orc.argmax_rows(orc.linear(A[:1], W, S, gs))[0])
+    lo = max(0, top - 777)
+    W[lo] = W[top]
+    S[lo] = S[top]
+    logits_ref = orc.linear(A, W, S, gs)
+    ids_ref = orc.argmax_rows(logits_ref)
+    assert ids_ref[0] == lo
+    logits = torch.empty((M, V), dtype=torch.float32, device="cuda")
+    ids = host(q.lm_head_argmax(dev(A), dev(W), dev(S), gs, logits=logits))
+    assert_bits_equal(host(logits), logits_ref, "logits")
+    np.testing.assert_array_equal(ids, ids_ref)
 
 
 def test_argmax_rows_special_values(orc):
