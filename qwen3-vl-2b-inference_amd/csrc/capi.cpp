@@ -197,7 +197,21 @@ int run_linear(const float *A, int nseg, const int8_t *const *W, const float *co
     int rc = resolve_ws(ws, wsb, L.total, &wbase);
     if (rc) return rc;
 
-    if (gemv_path_ok(M, K, gs)) {
+    // 5..8 rows against a very wide weight (the lm_head over a batch of
+    // rows): the MFMA GEMM, with the rows padded to one 32-row tile, streams
+    // the weights faster than the general GEMV's integer dot products.
+    bool wide_mf = M >= 5 && M <= 8 && gs == 64 && mode != GEMV_SWIGLU;
+    for (int i = 0; wide_mf && i < nseg; ++i)
+        wide_mf = !(G && G[i]) && (size_t)Ns[i] * K >= ((size_t)1 << 26) &&
+                  (size_t)Ns[i] * K <= 0x7fffffffULL;
+    if (wide_mf) {
+        int cus = 0;
+        rc = device_cus(&cus);
+        if (rc) return rc;
+        for (int i = 0; wide_mf && i < nseg; ++i)
+            wide_mf = gemm_mf_serves((int)M, (int)Ns[i], (int)K, false, cus);
+    }
+    if (gemv_path_ok(M, K, gs) && !wide_mf) {
         // Lane numerics apply per segment shape; segments sharing one launch
         // must agree on the path.
         const bool lanes = q3vl_uses_lane_path(M, Ns[0], K);
@@ -236,7 +250,8 @@ int run_linear(const float *A, int nseg, const int8_t *const *W, const float *co
         return fail(Q3VL_ERR_UNSUPPORTED,
                     "GEMM path needs group_size in {32,64,128} and K %% 64 == 0 "
                     "(M=%zu K=%zu group_size=%zu)", M, K, gs);
-    // M > 8 (or an M <= 8 shape the GEMV kernels do not take): quantize once.
+    // M > 8 (or an M <= 8 shape the GEMV kernels do not take or that runs
+    // faster on the GEMM): quantize once.
     const WsLayout LG = layout(M > 8 ? M : 9, Nmax, K, gs);
     if (LG.total > L.total) {
         rc = resolve_ws(ws, wsb, LG.total, &wbase);

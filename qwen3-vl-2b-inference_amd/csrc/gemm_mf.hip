@@ -32,9 +32,10 @@
 // * The k order inside a group: slice s of lane half h covers k = 32h + 8s +
 //   j; A and B use the same map, so each MFMA pairs matching k and the four
 //   slices cover the group's 64 k once.
-// * Block: 4 waves in 2 x 2, wave tile (32 TM) x (32 TN); two or three
+// * Block: 4 waves in WM x (4/WM), wave tile (32 TM) x (32 TN); two or three
 //   blocks share a CU, so one block's epilogue overlaps another's MFMAs and
 //   its loads another's waits. One barrier per group (an LDS-only fence).
+//   WM = 1 serves M <= 32 (one m-tile): all four waves take output columns.
 //   SWIGLU: the block's B rows are 32 TN gate rows and the same up rows; wave
 //   wn holds gate n-tile wn and up n-tile 2 + wn, so silu(gate) * up needs no
 //   exchange.
@@ -125,20 +126,22 @@ __device__ __forceinline__ int bslot(int s, int l) {
 // by the staging into LDS) before its slot is reloaded; a value copied out of
 // the ring into other registers would make each reload wait for that copy's
 // load, which the in-order return turns into a wait for the whole ring.
-template <int TM, int TN, bool SWIGLU, int D, int BPC>
+template <int TM, int TN, bool SWIGLU, int D, int BPC, int WM = 2>
 __global__ __launch_bounds__(256, BPC) void gemm_mf_kernel(GemmMfArgs a) {
-    constexpr int BM = 64 * TM;             // rows of the block
-    constexpr int BN = 64 * TN;             // weight rows of the block
+    constexpr int WN = 4 / WM;              // waves along N
+    constexpr int MTB = WM * TM;            // m-tiles of the block
+    constexpr int BN = 32 * WN * TN;        // weight rows of the block
     constexpr int NT = BN / 32;             // n-tiles in the B buffer
     constexpr int BCH = BN * 4 / 256;       // 16-byte weight chunks per thread and group
     constexpr int BBUF = NT * 4 * 64 * 16;  // bytes of one B buffer
-    static_assert(!SWIGLU || TN == 2, "SwiGLU pairs one gate and one up n-tile per wave");
+    static_assert(!SWIGLU || (TN == 2 && WM == 2), "SwiGLU pairs one gate and one up n-tile per wave");
+    static_assert(WM == 1 || WM == 2, "2 x 2 or 1 x 4 waves");
     extern __shared__ __align__(16) unsigned char smem[];
-    float *asl = reinterpret_cast<float *>(smem + 2 * BBUF);  // [3][2TM m-tiles][32]
-    float *wsl = asl + 3 * 64 * TM;                             // [3][BN]
+    float *asl = reinterpret_cast<float *>(smem + 2 * BBUF);  // [3][MTB m-tiles][32]
+    float *wsl = asl + 3 * 32 * MTB;                            // [3][BN]
 
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-    const int wm = wid & 1, wn = wid >> 1;
+    const int wm = wid % WM, wn = wid / WM;
     const int M = a.M, N = a.N, K = a.K, Kg = K / 64, Mt = a.Mt;
     const int ncols = SWIGLU ? BN / 2 : BN;  // output columns of the block
     // XCD-aware tile order. Workgroups go to the 8 XCDs round-robin (block b
@@ -146,13 +149,13 @@ __global__ __launch_bounds__(256, BPC) void gemm_mf_kernel(GemmMfArgs a) {
     // gives XCD x the contiguous tiles [x per, (x+1) per), taken M-tile
     // fastest: a few columns of weight rows (which then stay in that XCD's
     // L2) against all activation rows, read by the XCD's blocks in step.
-    const int tiles_m = (Mt + 2 * TM - 1) / (2 * TM);
+    const int tiles_m = (Mt + MTB - 1) / MTB;
     const int tiles = tiles_m * ((N + ncols - 1) / ncols);
     const int per = (tiles + 7) / 8;
     const int t = (int)(blockIdx.x % 8) * per + (int)(blockIdx.x / 8);
     if (t >= tiles) return;  // whole block: before any barrier
     const int n0 = (t / tiles_m) * ncols;
-    const int mt0 = (t % tiles_m) * 2 * TM;  // first m-tile of the block
+    const int mt0 = (t % tiles_m) * MTB;  // first m-tile of the block
 
     // Global loads go through buffer resources (SGPR base and size, 32-bit
     // per-lane offsets, the per-group advance in the scalar offset); a read
@@ -192,10 +195,10 @@ __global__ __launch_bounds__(256, BPC) void gemm_mf_kernel(GemmMfArgs a) {
         bdst0[i] = (nt * 256 + bslot(s0, l)) * 16;
         bdst1[i] = (nt * 256 + bslot(s0 + 1, l)) * 16;
     }
-    // ---- a_s staging: threads < 16 TM copy one float4 each (2 TM m-tiles of
+    // ---- a_s staging: threads < 8 MTB copy one float4 each (MTB m-tiles of
     // 32 scales per group)
     int as_off = 0, as_dst = 0;
-    const bool as_thr = tid < 16 * TM;
+    const bool as_thr = tid < 8 * MTB;
     if (as_thr) {
         const int i = tid >> 3, part = tid & 7;  // m-tile i of the block, 16 B piece
         const int mt = min(mt0 + i, Mt - 1);
@@ -239,7 +242,7 @@ __global__ __launch_bounds__(256, BPC) void gemm_mf_kernel(GemmMfArgs a) {
             braw[sl][i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
                                                         up ? rW1 : rW0, boff[i], 64 * g, 0));
         }
-        // (threads past the 2 TM m-tiles read scales at offset 128 g of the
+        // (threads past the MTB m-tiles read scales at offset 128 g of the
         // buffer and discard them: the scalar offset stays uniform)
         asraw[sl] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rAS, as_off, 128 * g, 0));
         wsraw[sl] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
@@ -261,7 +264,7 @@ __global__ __launch_bounds__(256, BPC) void gemm_mf_kernel(GemmMfArgs a) {
             *reinterpret_cast<u32x4 *>(Bs + bdst0[i]) = (u32x4){w[0], w[1], w[2], w[3]};
             *reinterpret_cast<u32x4 *>(Bs + bdst1[i]) = (u32x4){w[4], w[5], w[6], w[7]};
         }
-        if (as_thr) *reinterpret_cast<float4 *>(asl + (g % 3) * 64 * TM + as_dst) = asraw[sl];
+        if (as_thr) *reinterpret_cast<float4 *>(asl + (g % 3) * 32 * MTB + as_dst) = asraw[sl];
         if (ws_thr) wsl[(g % 3) * BN + tid] = wsraw[sl];
     };
 
@@ -302,7 +305,7 @@ __global__ __launch_bounds__(256, BPC) void gemm_mf_kernel(GemmMfArgs a) {
     };
     // epilogue of group g, reference order: out = fma(G * a_s, w_s, out)
     auto epilogue = [&](int g) {
-        const float *as_g = asl + (g % 3) * 64 * TM + wm * TM * 32 + h * 16;
+        const float *as_g = asl + (g % 3) * 32 * MTB + wm * TM * 32 + h * 16;
         float ws_g[TN];
 #pragma unroll
         for (int j = 0; j < TN; ++j) ws_g[j] = wsl[(g % 3) * BN + bt[j] * 32 + (lane & 31)];
@@ -367,25 +370,27 @@ __global__ __launch_bounds__(256, BPC) void gemm_mf_kernel(GemmMfArgs a) {
     }
 }
 
-template <int TM, int TN, bool SWIGLU, int D, int BPC>
+template <int TM, int TN, bool SWIGLU, int D, int BPC, int WM = 2>
 static hipError_t launch_mf(const GemmMfArgs &a, hipStream_t st) {
-    constexpr int BN = 64 * TN;
+    constexpr int BN = 32 * (4 / WM) * TN, MTB = WM * TM;
     const int ncols = SWIGLU ? BN / 2 : BN;
-    const int tiles = ((a.N + ncols - 1) / ncols) * ((a.Mt + 2 * TM - 1) / (2 * TM));
+    const int tiles = ((a.N + ncols - 1) / ncols) * ((a.Mt + MTB - 1) / MTB);
     const int grid = 8 * ((tiles + 7) / 8);  // see the tile order in the kernel
-    const size_t lds = 2 * (BN / 32) * 4 * 64 * 16 + 3 * 64 * TM * 4 + 3 * BN * 4;
-    gemm_mf_kernel<TM, TN, SWIGLU, D, BPC><<<grid, 256, lds, st>>>(a);
+    const size_t lds = 2 * (BN / 32) * 4 * 64 * 16 + 3 * 32 * MTB * 4 + 3 * BN * 4;
+    gemm_mf_kernel<TM, TN, SWIGLU, D, BPC, WM><<<grid, 256, lds, st>>>(a);
     return hipGetLastError();
 }
 
 // Where this kernel serves (the caller quantizes in fragment order for it)
-// and with which tiles, from timings of the prefill and vision shapes on
-// MI355X. SwiGLU: always; 64 x (64 gate + 64 up) tiles at 3 blocks per CU
-// while the grid fits one round of the device, else 128-row tiles. Plain:
-// while 64 x 64 tiles give every CU at least two blocks; 128 x 64 tiles once
-// those give every CU about two. Long-K shapes with fewer tiles (down_proj at
-// M = 512, the vision fc2 and merger at K = 4096) run faster on
-// gemm_g64_kernel, whose A tiles go through LDS.
+// and with which tiles, from timings of the prefill, vision and lm_head
+// shapes on MI355X. SwiGLU: always; 64 x (64 gate + 64 up) tiles at 3 blocks
+// per CU while the grid fits one round of the device, else 128-row tiles.
+// Plain: while 64 x 64 tiles give every CU at least two blocks; one m-tile
+// (M <= 32, e.g. the lm_head over a few rows) takes 32 x 128 tiles of 1 x 4
+// waves, more m-tiles 128 x 64 tiles once those give every CU about two.
+// Long-K shapes with fewer tiles (down_proj at M = 512, the vision fc2 and
+// merger at K = 4096) run faster on gemm_g64_kernel, whose A tiles go
+// through LDS.
 static long mf_blocks(const GemmMfArgs &a, int tm, int ncols) {
     return (long)((a.N + ncols - 1) / ncols) * ((a.Mt + 2 * tm - 1) / (2 * tm));
 }
@@ -405,6 +410,7 @@ hipError_t launch_gemm_mf(const GemmMfArgs &a, bool swiglu, int cus, hipStream_t
         if (mf_blocks(a, 1, 64) <= 3L * cus) return launch_mf<1, 2, true, 1, 3>(a, st);
         return launch_mf<2, 2, true, 1, 2>(a, st);
     }
+    if (a.Mt == 1) return launch_mf<1, 1, false, 2, 3, 1>(a, st);
     if (4 * mf_blocks(a, 2, 64) >= 7L * cus) return launch_mf<2, 1, false, 2, 2>(a, st);
     return launch_mf<1, 1, false, 2, 2>(a, st);
 }

@@ -120,7 +120,8 @@ def test_gemm_parity(orc, M, N, K, gs):
     run_linear_case(orc, M, N, K, gs, seed=M + N + K, groups=M * N * K <= 64 * 512 * 2048)
 
 
-@pytest.mark.parametrize("M,N,K", [(9, 128, 1024), (100, 200, 2048), (130, 260, 1024),
+@pytest.mark.parametrize("M,N,K", [(9, 128, 1024), (100, 200, 2048), (130, 260, 1024), (7, 65600, 1024),
+                                   (17, 33000, 1024),
                                    (784, 3072, 1024), (196, 2048, 4096), (512, 8192, 1024),
                                    (513, 8200, 1024), (512, 2048, 6144), (1030, 8200, 128),
                                    (1024, 8192, 256)])
@@ -260,10 +261,13 @@ def test_lm_head_argmax_parity(orc, M):
     np.testing.assert_array_equal(ids2, ids_ref)
 
 
-@pytest.mark.parametrize("M,V,K", [(12, 5000, 1024), (40, 33000, 2048)])
+@pytest.mark.parametrize("M,V,K", [(12, 5000, 1024), (40, 33000, 2048), (6, 70001, 1024),
+                                   (20, 40000, 2048), (32, 33000, 2048)])
 def test_lm_head_argmax_gemm_path(orc, M, V, K):
-    """lm_head + argmax for M > 8 (the GEMM, then the row argmax), with a
-    planted tie that the lowest index must win, logits bit-exact."""
+    """lm_head + argmax on the GEMM (then the row argmax): M > 8, and 5..8
+    rows against a very wide weight; one m-tile (M <= 32) takes the 1 x 4
+    wave tiles. A planted tie that the lowest index must win, logits
+    bit-exact."""
     gs = 64
     A, W, S = make_case(77 + M, M, V, K, gs)
     top = int(orc.argmax_rows(orc.linear(A[:1], W, S, gs))[0])
