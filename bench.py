@@ -418,9 +418,13 @@ def build_model(dims, seed):
     return m, k16, v16
 
 
-def bench_cfg1(args, m, k16, v16, dims):
+def bench_cfg1(args, m, k16, v16, dims, chunked=False):
+    """The decode step in a HIP graph. chunked: the chunked attention order
+    (Q3VL_ATTN_CHUNKED) in place of the reference's, reported beside the
+    headline (the headline keeps the reference order)."""
     import torch
     from q3vl_int8 import model as qm
+    dims = dict(dims, attn_order=qm.ATTN_CHUNKED if chunked else qm.ATTN_REFERENCE)
     model = qm.DeviceTextModel(dims, m)
     kd = torch.from_numpy(k16.view("int16")).cuda()
     vd = torch.from_numpy(v16.view("int16")).cuda()
@@ -459,13 +463,19 @@ def bench_cfg1(args, m, k16, v16, dims):
     end_pos = int(pos.item())
     assert end_pos == CTX + args.warmup + args.steps, (end_pos, args.warmup, args.steps)
     step_bytes = decode_step_bytes(dims, CTX + args.warmup + args.steps // 2)
-    res = dict(name="cfg1_decode_step", metric="tok/s", value=1000.0 / ms, ms=ms,
+    res = dict(name="cfg1_decode_step_chunked_attention" if chunked else "cfg1_decode_step",
+               metric="tok/s", value=1000.0 / ms, ms=ms,
                eager_ms=eager_ms, contexts=[CTX + args.warmup, end_pos - 1],
                bytes_per_token=step_bytes, bytes_roofline_tok_s=HBM_PEAK_GBS * 1e9 / step_bytes,
                frac_of_bytes_roofline=(1000.0 / ms) / (HBM_PEAK_GBS * 1e9 / step_bytes),
                kernel_launches_per_token=decode_launches(dims))
     del g
-    res["gemv_roofline"] = decode_gemv_roofline(model, dims)
+    if chunked:
+        res["attention_order"] = ("chunked: per 64-position chunk a max, sum and value chain, folded "
+                                  "over the chunks (no counterpart in the reference; within the "
+                                  "reference's exp256 error of its order)")
+    else:
+        res["gemv_roofline"] = decode_gemv_roofline(model, dims)
     return res
 
 
@@ -829,7 +839,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200, help="timed decode steps (tokens)")
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--configs", default="cfg1,cfg0,cfg2,cfg3,cfg4,export")
+    ap.add_argument("--configs", default="cfg1,cfg1c,cfg0,cfg2,cfg3,cfg4,export")
     ap.add_argument("--cpu-budget", type=float, default=15.0,
                     help="seconds of reference CPU decode for cpu_baseline; the linear() "
                          "figures get a third of it each (0: skip the CPU leg)")
@@ -875,15 +885,20 @@ def main():
         "load": lambda: [bench_load(args)],
     }
     for c in configs:
-        if c != "cfg1" and c not in runners:
-            raise SystemExit(f"unknown config {c!r} (cfg0..cfg4, export, load)")
+        if c not in ("cfg1", "cfg1c") and c not in runners:
+            raise SystemExit(f"unknown config {c!r} (cfg0..cfg4, cfg1c, export, load)")
+    decode_model = None
     for c in configs:
         log("bench:", c)
         try:
-            if c == "cfg1":
-                m, k16, v16 = build_model(dims, MODEL_SEED)
-                out = [bench_cfg1(args, m, k16, v16, dims)]
+            if c in ("cfg1", "cfg1c"):
+                if decode_model is None:
+                    decode_model = build_model(dims, MODEL_SEED)
+                m, k16, v16 = decode_model
+                out = [bench_cfg1(args, m, k16, v16, dims, chunked=c == "cfg1c")]
                 del m, k16, v16
+                if not ({"cfg1", "cfg1c"} - set(configs[:configs.index(c) + 1])):
+                    decode_model = None  # both decode configs done
             else:
                 out = runners[c]()
         except Exception as e:  # noqa: BLE001 -- one config's failure is recorded, not fatal

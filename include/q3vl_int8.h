@@ -77,9 +77,10 @@ enum q3vl_dtype {
 
 /* Message of this thread's last failing call ("" if none). */
 const char *q3vl_last_error(void);
-/* ABI version of this header (bumped on any signature change). */
+/* ABI version of this header (bumped on any signature or struct layout
+ * change; 3: q3vl_text_model.attn_order). */
 int q3vl_abi_version(void);
-#define Q3VL_ABI_VERSION 2
+#define Q3VL_ABI_VERSION 3
 
 /* Scratch bytes needed by q3vl_linear_i8* / q3vl_lm_head_argmax for a shape. */
 size_t q3vl_workspace_bytes(size_t M, size_t N, size_t K, size_t group_size);
@@ -171,7 +172,20 @@ typedef struct q3vl_text_model {
     const int8_t *wq, *wk, *wv, *wo, *wg, *wu, *wd;        /* [layers, N, K] */
     const float *sq, *sk, *sv, *so, *sg, *su, *sd;         /* [layers, N, K/gs] */
     const float *rope_cos, *rope_sin;                      /* [max_seq, head_dim/2] */
+    /* Order of the attention's softmax and value sum. Q3VL_ATTN_REFERENCE
+     * (0, what a zero-initialized struct holds): the reference's
+     * (text_layer.cpp:436-535, 655-710) -- one max, sum and value chain over
+     * all positions. Q3VL_ATTN_CHUNKED (1): no counterpart in the reference;
+     * per 64-position chunk a max, a sum and a value chain, folded chunk by
+     * chunk. It differs from the reference order by the error of the
+     * reference's exp256 polynomial (up to a few 1e-4 of the output scale;
+     * each order is that far from an exact softmax), and the test oracle
+     * restates it exactly. */
+    int attn_order;
 } q3vl_text_model;
+
+#define Q3VL_ATTN_REFERENCE 0
+#define Q3VL_ATTN_CHUNKED 1
 
 /* Scratch bytes q3vl_decode_step needs for a model. */
 size_t q3vl_decode_workspace_bytes(const q3vl_text_model *m);

@@ -262,12 +262,79 @@ void orc_attention(const float *q, const float *kc, const float *vc, size_t head
     }
 }
 
+/* The chunked attention order (no counterpart in the reference; the GPU's
+ * Q3VL_ATTN_CHUNKED): scores as orc_attention computes them, then per query
+ * head and 64-position chunk c (positions t of the chunk below pos + 1):
+ *   m_c = max of the chunk's scores (fmaxf from -inf),
+ *   e_t = exp256(s_t - m_c), 0 for s_t = -inf or m_c not finite, and 0 for
+ *         the chunk's slots past the context,
+ *   l_c = xor butterfly over the chunk's 64 slots: for offsets 32, 16, 8, 4,
+ *         2, 1 every slot i becomes slot i + slot (i ^ offset); slot 0,
+ *   o_c[d] = fmaf chain over the chunk's t ascending of e_t * v_t[d];
+ * then, over the chunks ascending: M = max_c m_c, w_c = exp256(m_c - M) (0
+ * for m_c = -inf or M not finite), L and O[d] fmaf chains of w_c * l_c and
+ * w_c * o_c[d], out[d] = O[d] * (1.0f / L) when L is finite and positive,
+ * else 0. */
+void orc_attention_chunked(const float *q, const float *kc, const float *vc, size_t heads,
+                           size_t kv_heads, size_t hd, size_t max_seq, size_t pos, float *att,
+                           float *out) {
+    const size_t kv_mul = heads / kv_heads, n = pos + 1, nch = (n + 63) / 64;
+    const float inv_sqrt_d = 1.0f / sqrtf((float)hd);
+    float *mc = malloc(nch * 4), *lc = malloc(nch * 4), *oc = malloc(nch * hd * 4);
+    for (size_t h = 0; h < heads; ++h) {
+        const float *qh = q + h * hd;
+        const float *kh = kc + (h / kv_mul) * max_seq * hd;
+        const float *vh = vc + (h / kv_mul) * max_seq * hd;
+        for (size_t t = 0; t <= pos; ++t) att[t] = dot_lanes(qh, kh + t * hd, hd) * inv_sqrt_d;
+        for (size_t t = pos / 8 * 8; t <= pos; ++t)
+            att[t] = dot_tail(qh, kh + t * hd, hd) * inv_sqrt_d;
+        for (size_t c = 0; c < nch; ++c) {
+            const size_t t0 = 64 * c, rows = n - t0 < 64 ? n - t0 : 64;
+            float m = -INFINITY;
+            for (size_t i = 0; i < rows; ++i) m = fmaxf(m, att[t0 + i]);
+            float e[64];
+            for (size_t i = 0; i < 64; ++i)
+                e[i] = (i < rows && att[t0 + i] > -INFINITY && isfinite(m))
+                           ? orc_exp256(att[t0 + i] - m) : 0.0f;
+            float b[64];
+            memcpy(b, e, sizeof b);
+            for (size_t off = 32; off > 0; off >>= 1) {
+                float nb[64];
+                for (size_t i = 0; i < 64; ++i) nb[i] = b[i] + b[i ^ off];
+                memcpy(b, nb, sizeof b);
+            }
+            mc[c] = m;
+            lc[c] = b[0];
+            for (size_t d = 0; d < hd; ++d) {
+                float acc = 0.0f;
+                for (size_t i = 0; i < rows; ++i) acc = fmaf(e[i], vh[(t0 + i) * hd + d], acc);
+                oc[c * hd + d] = acc;
+            }
+        }
+        float M = -INFINITY;
+        for (size_t c = 0; c < nch; ++c) M = fmaxf(M, mc[c]);
+        for (size_t d = 0; d < hd; ++d) {
+            float L = 0.0f, O = 0.0f;
+            for (size_t c = 0; c < nch; ++c) {
+                const float w = (isfinite(M) && mc[c] > -INFINITY) ? orc_exp256(mc[c] - M) : 0.0f;
+                L = fmaf(w, lc[c], L);
+                O = fmaf(w, oc[c * hd + d], O);
+            }
+            out[h * hd + d] = (L > 0.0f && isfinite(L)) ? O * (1.0f / L) : 0.0f;
+        }
+    }
+    free(mc), free(lc), free(oc);
+}
+
 /* model/src/forward.cpp:458-720 forward_text for a text token at `pos`.
- * kv_fp16 != 0: the caches hold fp16 bits (uint16) and new K/V rows are
- * rounded to fp16 on store; kv_fp16 == 0: fp32 caches as in the reference
- * (lm:348-349). Returns greedy_decode(logits); logits [vocab] if non-null. */
-int32_t orc_decode_step(const orc_model *m, void *k_cache, void *v_cache, int kv_fp16,
+ * flags bit 0 (ORC_KV_FP16): the caches hold fp16 bits (uint16) and new K/V
+ * rows are rounded to fp16 on store; clear: fp32 caches as in the reference
+ * (lm:348-349). Bit 1 (ORC_ATTN_CHUNKED): orc_attention_chunked in place of
+ * the reference's attention. Returns greedy_decode(logits); logits [vocab]
+ * if non-null. */
+int32_t orc_decode_step(const orc_model *m, void *k_cache, void *v_cache, int flags,
                         int32_t token, size_t pos, float *logits) {
+    const int kv_fp16 = flags & ORC_KV_FP16;
     const size_t H = (size_t)m->hidden, I = (size_t)m->inter, NH = (size_t)m->heads;
     const size_t NKV = (size_t)m->kv_heads, D = (size_t)m->head_dim, S = (size_t)m->max_seq;
     const size_t gs = (size_t)m->gs, V = (size_t)m->vocab, L = (size_t)m->layers;
@@ -319,7 +386,10 @@ int32_t orc_decode_step(const orc_model *m, void *k_cache, void *v_cache, int kv
                     }
                 }
         /* :571-581 attention */
-        orc_attention(q, kl, vl, NH, NKV, D, S, pos, att, ao);
+        if (flags & ORC_ATTN_CHUNKED)
+            orc_attention_chunked(q, kl, vl, NH, NKV, D, S, pos, att, ao);
+        else
+            orc_attention(q, kl, vl, NH, NKV, D, S, pos, att, ao);
         /* :592-604 output projection + residual */
         orc_linear_i8(ao, m->wo + l * H * QD, m->so + l * H * QD / gs, t, NULL, 1, H, QD, gs);
         for (size_t i = 0; i < H; ++i) x[i] += t[i];

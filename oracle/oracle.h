@@ -99,7 +99,12 @@ void orc_softmax(float *x, size_t n);
 void orc_attention(const float *q, const float *kc, const float *vc, size_t heads,
                    size_t kv_heads, size_t hd, size_t max_seq, size_t pos, float *att,
                    float *out);
-int32_t orc_decode_step(const orc_model *m, void *k_cache, void *v_cache, int kv_fp16,
+void orc_attention_chunked(const float *q, const float *kc, const float *vc, size_t heads,
+                           size_t kv_heads, size_t hd, size_t max_seq, size_t pos, float *att,
+                           float *out);
+#define ORC_KV_FP16 1
+#define ORC_ATTN_CHUNKED 2
+int32_t orc_decode_step(const orc_model *m, void *k_cache, void *v_cache, int flags,
                         int32_t token, size_t pos, float *logits);
 
 #ifdef __cplusplus

@@ -372,7 +372,7 @@ void reg_free(RegEntry &e) {
 // ------------------------------------------------------------ decode step
 struct DecodeLayout {
     size_t lin;  // linear() scratch (argmax partials)
-    size_t x, q, k, v, ao, h, scores, cmax;
+    size_t x, q, k, v, ao, h, scores, cmax, part_o, part_ml;
     size_t total;
     int max_chunks;
 };
@@ -397,6 +397,10 @@ DecodeLayout decode_layout(const q3vl_text_model *m) {
     L.h = take(I * 4);
     L.scores = take(NH * S * 4);
     L.cmax = take(NH * (size_t)L.max_chunks * 4);
+    // the chunked attention order's per-chunk partials
+    const bool chunked = m->attn_order == Q3VL_ATTN_CHUNKED;
+    L.part_o = chunked ? take(NH * (size_t)L.max_chunks * D * 4) : 0;
+    L.part_ml = chunked ? take(NH * (size_t)L.max_chunks * 2 * 4) : 0;
     L.total = off;
     return L;
 }
@@ -417,6 +421,9 @@ int check_model_dims(const q3vl_text_model *m) {
         return fail(Q3VL_ERR_UNSUPPORTED, "group_size %ld not served", gs);
     if (m->vocab < 1024 || m->layers < 1 || m->max_seq < 8 || m->max_seq % 8)
         return fail(Q3VL_ERR_INVALID_ARGUMENT, "bad vocab / layers / max_seq (a multiple of 8)");
+    if (m->attn_order != Q3VL_ATTN_REFERENCE && m->attn_order != Q3VL_ATTN_CHUNKED)
+        return fail(Q3VL_ERR_INVALID_ARGUMENT, "attn_order %d is neither Q3VL_ATTN_REFERENCE nor "
+                    "Q3VL_ATTN_CHUNKED", m->attn_order);
     if (attention_lds_bytes(m->heads, m->kv_heads, m->max_seq) > kAttnMaxLds)
         return fail(Q3VL_ERR_UNSUPPORTED,
                     "max_seq %d too long for the attention kernel's LDS (heads/kv_heads %d)",
@@ -688,6 +695,11 @@ int decode_step_on(const q3vl_text_model *m, uint16_t *k_cache, uint16_t *v_cach
     aa.pos = pos;
     aa.scores = F(L.scores);
     aa.cmax = F(L.cmax);
+    aa.order = m->attn_order;
+    if (m->attn_order == Q3VL_ATTN_CHUNKED) {
+        aa.part_o = F(L.part_o);
+        aa.part_ml = F(L.part_ml);
+    }
     aa.out = ao;
     aa.heads = NH;
     aa.kv_heads = NKV;

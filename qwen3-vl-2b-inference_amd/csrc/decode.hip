@@ -142,22 +142,6 @@ struct NormRopeIn {
     float c, s;    // rope cos / sin at (pos, lane)
 };
 
-__device__ __forceinline__ NormRopeIn load_norm_rope(const float *x, const int8_t *w,
-                                                     const float *ws, int gs,
-                                                     const float *cosr, const float *sinr,
-                                                     int lane) {
-    NormRopeIn r;
-    r.lo = x[lane];
-    r.hi = x[lane + 64];
-    r.wl = w[lane];
-    r.wh = w[lane + 64];
-    r.sl = ws[lane / gs];
-    r.sh = ws[(lane + 64) / gs];
-    r.c = cosr[lane];
-    r.s = sinr[lane];
-    return r;
-}
-
 __device__ __forceinline__ void norm_rope128(const NormRopeIn &in, float eps, float &lo, float &hi) {
     // opaque copies: keeps the int8 -> float conversions (and their waits)
     // here rather than next to the loads
@@ -197,53 +181,95 @@ __global__ __launch_bounds__(256) void embed_kernel(const int8_t *w, const float
 // 548-562). Scores follow text_layer.cpp:598-620 exactly: 8 FMA lane chains
 // over the head dimension, the fixed tree (the left-to-right fold for the
 // positions of the last partial block of 8), times 1/sqrt(hd).
+//
+// PAR (the chunked order, Q3VL_ATTN_CHUNKED; no counterpart in the
+// reference, whose softmax and value sum run over all positions in one
+// order): the block also forms its chunk's share of the softmax and of the
+// value sum, per query head h and chunk c (positions t of the chunk, t < n):
+//   m_c = max of the chunk's scores,
+//   e_t = exp256(s_t - m_c)  (0 for s_t = -inf or m_c not finite),
+//   l_c = the e_t of the 64 lanes (0 past the context) summed by the xor
+//         butterfly, offsets 32, 16, 8, 4, 2, 1 (each lane adds the partner
+//         lane's value to its own),
+//   o_c[d] = fma chain over the chunk's t ascending of e_t * v_t[d];
+// attn_combine_kernel folds the chunks. A value chain is then at most 64
+// steps instead of pos + 1.
 constexpr int ATT_CH = 64;
 constexpr int ATT_HD = 128;
 constexpr int ATT_KSTR = ATT_HD + 8;  // halves per LDS key row (272 B: bank-spread)
 constexpr int ATT_THREADS = 256;
 constexpr int ATT_KITEMS = ATT_CH * (ATT_HD / 8) / ATT_THREADS;  // 16-byte key pieces per thread
 
+template <bool PAR>
 __global__ __launch_bounds__(ATT_THREADS) void attn_scores_kernel(AttnArgs a) {
     __shared__ float qsh[3][ATT_HD];
     __shared__ uint16_t ksh[ATT_CH * ATT_KSTR];
     __shared__ __align__(16) uint16_t knew[ATT_HD];
+    __shared__ __align__(16) uint16_t vnew[PAR ? ATT_HD : 1];
+    __shared__ __align__(16) uint32_t vsh[PAR ? ATT_CH / 2 * ATT_HD : 1];  // [t/2][d]: (v_2r[d], v_2r+1[d])
+    __shared__ __align__(16) float esh[PAR ? 3 : 1][ATT_CH];
     const int kvh = blockIdx.x, ch = blockIdx.y;
-    const int pos = *a.pos;
-    if (pos < 0 || pos >= a.max_seq) return;  // no cache row for it: nothing is touched
-    const int n = pos + 1;
-    const int t0 = ch * ATT_CH;
-    if (t0 >= n) return;  // uniform: chunk past the context
     const int kvm = a.heads / a.kv_heads;
+    const int S = a.max_seq;
     const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63;
-    const size_t lay = ((size_t)a.layer * a.kv_heads + kvh) * a.max_seq * ATT_HD;
+    const int t0 = ch * ATT_CH;
+    const size_t lay = ((size_t)a.layer * a.kv_heads + kvh) * S * ATT_HD;
     uint16_t *kc = a.k_cache + lay;
     uint16_t *vc = a.v_cache + lay;
-    const bool own_pos = pos >= t0 && pos < t0 + ATT_CH;
-    const bool nr_q = wid < kvm, nr_k = wid == kvm && own_pos;
+    const bool q_wave = wid < kvm, k_wave = wid == kvm;
 
-    // Issue order: the norm/rope inputs, then the key tile (vmcnt retires in
-    // order, so the norm waits only for its own loads).
+    // Loads that need no `pos` go out first, so that their latency overlaps
+    // that of `pos` itself: the norm inputs of the query heads (and of the
+    // new key and value), then the key tile (and the value tile) with rows
+    // clamped into the cache -- rows at or past the context are replaced
+    // when staged. vmcnt retires in order, so the norms wait only for their
+    // own loads.
     NormRopeIn nri{};
     float vlo = 0.0f, vhi = 0.0f;
-    if (nr_q || nr_k) {
-        const float *cosr = a.rope_cos + (size_t)pos * (ATT_HD / 2);
-        const float *sinr = a.rope_sin + (size_t)pos * (ATT_HD / 2);
-        if (nr_q) {
-            nri = load_norm_rope(a.q + (kvh * kvm + wid) * ATT_HD, a.qnorm_w, a.qnorm_s, a.gs,
-                                 cosr, sinr, lane);
-        } else {
-            nri = load_norm_rope(a.k + kvh * ATT_HD, a.knorm_w, a.knorm_s, a.gs, cosr, sinr, lane);
+    if (q_wave || k_wave) {
+        const float *x = q_wave ? a.q + (kvh * kvm + wid) * ATT_HD : a.k + kvh * ATT_HD;
+        const int8_t *w = q_wave ? a.qnorm_w : a.knorm_w;
+        const float *ws = q_wave ? a.qnorm_s : a.knorm_s;
+        nri.lo = x[lane];
+        nri.hi = x[lane + 64];
+        nri.wl = w[lane];
+        nri.wh = w[lane + 64];
+        nri.sl = ws[lane / a.gs];
+        nri.sh = ws[(lane + 64) / a.gs];
+        if (k_wave) {
             vlo = a.v[kvh * ATT_HD + lane];
             vhi = a.v[kvh * ATT_HD + 64 + lane];
         }
     }
-    __builtin_amdgcn_sched_barrier(0);
-    // key tile rows clamped into the context; row pos is replaced by knew
     u32x4 kr[ATT_KITEMS];
 #pragma unroll
     for (int it = 0; it < ATT_KITEMS; ++it) {
         const int idx = it * ATT_THREADS + tid, r = idx >> 4, c8 = idx & 15;
-        kr[it] = *reinterpret_cast<const u32x4 *>(kc + (size_t)min(t0 + r, n - 1) * ATT_HD + c8 * 8);
+        kr[it] = *reinterpret_cast<const u32x4 *>(kc + (size_t)min(t0 + r, S - 1) * ATT_HD + c8 * 8);
+    }
+    // PAR: the value tile, by row pairs -- piece it of thread tid is pair
+    // rp = (it*256 + tid) / 16, dims 8 * (tid % 16) .. + 7 of both rows
+    constexpr int VIT = PAR ? ATT_CH / 2 * (ATT_HD / 8) / ATT_THREADS : 1;
+    u32x4 vr[VIT][2];
+    if constexpr (PAR) {
+#pragma unroll
+        for (int it = 0; it < VIT; ++it) {
+            const int idx = it * ATT_THREADS + tid, rp = idx >> 4, c8 = idx & 15;
+#pragma unroll
+            for (int o = 0; o < 2; ++o)
+                vr[it][o] = *reinterpret_cast<const u32x4 *>(vc + (size_t)min(t0 + 2 * rp + o, S - 1) * ATT_HD + c8 * 8);
+        }
+    }
+
+    const int pos = *a.pos;
+    if (pos < 0 || pos >= S) return;  // no cache row for it: nothing is touched
+    const int n = pos + 1;
+    if (t0 >= n) return;  // uniform: chunk past the context
+    const bool own_pos = pos >= t0 && pos < t0 + ATT_CH;
+    const bool nr_q = q_wave, nr_k = k_wave && own_pos;
+    if (nr_q || nr_k) {  // the rope row of pos
+        nri.c = a.rope_cos[(size_t)pos * (ATT_HD / 2) + lane];
+        nri.s = a.rope_sin[(size_t)pos * (ATT_HD / 2) + lane];
     }
     __builtin_amdgcn_sched_barrier(0);
 
@@ -260,10 +286,15 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_scores_kernel(AttnArgs a) {
         kc[(size_t)pos * ATT_HD + 64 + lane] = h16;
         knew[lane] = l16;
         knew[lane + 64] = h16;
-        vc[(size_t)pos * ATT_HD + lane] = f2h(vlo);
-        vc[(size_t)pos * ATT_HD + 64 + lane] = f2h(vhi);
+        const uint16_t vl16 = f2h(vlo), vh16 = f2h(vhi);
+        vc[(size_t)pos * ATT_HD + lane] = vl16;
+        vc[(size_t)pos * ATT_HD + 64 + lane] = vh16;
+        if constexpr (PAR) {
+            vnew[lane] = vl16;
+            vnew[lane + 64] = vh16;
+        }
     }
-    lds_barrier();  // knew
+    lds_barrier();  // knew, vnew
 #pragma unroll
     for (int it = 0; it < ATT_KITEMS; ++it) {
         const int idx = it * ATT_THREADS + tid, r = idx >> 4, c8 = idx & 15;
@@ -273,8 +304,35 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_scores_kernel(AttnArgs a) {
         else if (t == pos) v = *reinterpret_cast<const u32x4 *>(knew + c8 * 8);
         *reinterpret_cast<u32x4 *>(ksh + r * ATT_KSTR + c8 * 8) = v;
     }
-    lds_barrier();  // ksh, qsh
-    if (wid >= kvm) return;
+    if constexpr (PAR) {
+        // pairs (v_2rp[d], v_2rp+1[d]); rows past the context as zeros, row
+        // pos from vnew
+#pragma unroll
+        for (int it = 0; it < VIT; ++it) {
+            const int idx = it * ATT_THREADS + tid, rp = idx >> 4, c8 = idx & 15;
+            u32x4 rw[2];
+#pragma unroll
+            for (int o = 0; o < 2; ++o) {
+                const int t = t0 + 2 * rp + o;
+                rw[o] = vr[it][o];
+                if (t >= n) rw[o] = (u32x4){0u, 0u, 0u, 0u};
+                else if (t == pos) rw[o] = *reinterpret_cast<const u32x4 *>(vnew + c8 * 8);
+            }
+            const uint32_t l4[4] = {rw[0].x, rw[0].y, rw[0].z, rw[0].w};
+            const uint32_t h4[4] = {rw[1].x, rw[1].y, rw[1].z, rw[1].w};
+            uint32_t w[8];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                w[2 * k] = __builtin_amdgcn_perm(h4[k], l4[k], 0x05040100u);      // dim 2k
+                w[2 * k + 1] = __builtin_amdgcn_perm(h4[k], l4[k], 0x07060302u);  // dim 2k+1
+            }
+            uint32_t *dst = vsh + rp * ATT_HD + c8 * 8;
+            *reinterpret_cast<u32x4 *>(dst) = (u32x4){w[0], w[1], w[2], w[3]};
+            *reinterpret_cast<u32x4 *>(dst + 4) = (u32x4){w[4], w[5], w[6], w[7]};
+        }
+    }
+    lds_barrier();  // ksh, qsh, vsh
+    if (wid < kvm) {
     const int h = kvh * kvm + wid;
     const int t = t0 + lane;
     const int rows = min(ATT_CH, n - t0);
@@ -307,6 +365,126 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_scores_kernel(AttnArgs a) {
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
     if (lane == 0) a.cmax[h * a.max_chunks + ch] = m;
+    if constexpr (PAR) {
+        const float e = (lane < rows && score > -INFINITY && __builtin_isfinite(m)) ? exp256(score - m) : 0.0f;
+        esh[wid][lane] = e;
+        float l = e;
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) l = l + __shfl_xor(l, off);
+        if (lane == 0) {
+            a.part_ml[((size_t)h * a.max_chunks + ch) * 2] = m;
+            a.part_ml[((size_t)h * a.max_chunks + ch) * 2 + 1] = l;
+        }
+    }
+    }
+    if constexpr (PAR) {
+        lds_barrier();  // esh
+        // the chunk's value chains: thread tid runs query head tid / 128 of
+        // the group at dim tid % 128; with three query heads per kv head,
+        // threads below 128 also run head 2 at the same dim
+        const int dA = tid & (ATT_HD - 1), hA = tid >> 7;
+        const bool runA = hA < kvm, runB = kvm == 3 && tid < ATT_HD;
+        const int rows4 = (min(ATT_CH, n - t0) + 3) & ~3;  // e and V are zero past the context
+        float accA = 0.0f, accB = 0.0f;
+        if (runA) {
+            const float *eA = esh[min(hA, kvm - 1)], *eB = esh[min(2, kvm - 1)];
+            for (int t = 0; t < rows4; t += 4) {
+                const float4 pa = *reinterpret_cast<const float4 *>(eA + t);
+                const uint32_t v01 = vsh[(t / 2) * ATT_HD + dA], v23 = vsh[(t / 2 + 1) * ATT_HD + dA];
+                const float v0 = h2f((uint16_t)(v01 & 0xFFFFu)), v1 = h2f((uint16_t)(v01 >> 16));
+                const float v2 = h2f((uint16_t)(v23 & 0xFFFFu)), v3 = h2f((uint16_t)(v23 >> 16));
+                accA = fmaf(pa.x, v0, accA);
+                accA = fmaf(pa.y, v1, accA);
+                accA = fmaf(pa.z, v2, accA);
+                accA = fmaf(pa.w, v3, accA);
+                if (runB) {
+                    const float4 pb = *reinterpret_cast<const float4 *>(eB + t);
+                    accB = fmaf(pb.x, v0, accB);
+                    accB = fmaf(pb.y, v1, accB);
+                    accB = fmaf(pb.z, v2, accB);
+                    accB = fmaf(pb.w, v3, accB);
+                }
+            }
+            a.part_o[((size_t)(kvh * kvm + hA) * a.max_chunks + ch) * ATT_HD + dA] = accA;
+            if (runB) a.part_o[((size_t)(kvh * kvm + 2) * a.max_chunks + ch) * ATT_HD + dA] = accB;
+        }
+    }
+}
+
+// The chunked order's fold (PAR above), per query head h and dim d, chunks
+// c ascending:
+//   M = max_c m_c, w_c = exp256(m_c - M) (0 for m_c = -inf or M not finite),
+//   L = fma chain of w_c * l_c, O[d] = fma chain of w_c * o_c[d],
+//   out[d] = O[d] * (1.0f / L), or 0 where L is not finite and positive.
+// One block of 128 threads per query head. Every load is issued before the
+// values it feeds are needed: the (m_c, l_c) pairs of all chunks go to LDS
+// in one pass (one chunk per thread), the o_c[d] in batches of 16.
+constexpr int ATT_MAX_CHUNKS = 256;  // max_seq <= 16384
+__global__ __launch_bounds__(ATT_HD) void attn_combine_kernel(AttnArgs a) {
+    __shared__ float wsh[ATT_MAX_CHUNKS], lsh[ATT_MAX_CHUNKS], msh[ATT_MAX_CHUNKS];
+    __shared__ float mred[2];
+    const int h = blockIdx.x, d = threadIdx.x, lane = d & 63;
+    const float *ml = a.part_ml + (size_t)h * a.max_chunks * 2;
+    const float *po = a.part_o + (size_t)h * a.max_chunks * ATT_HD + d;
+    // the first chunks' partials go out before `pos` is known (indices
+    // clamped into the buffers; chunks past the context are not used)
+    const float2 ml0 = *reinterpret_cast<const float2 *>(ml + 2 * min(d, a.max_chunks - 1));
+    float ob[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) ob[i] = po[(size_t)min(i, a.max_chunks - 1) * ATT_HD];
+    const int pos = *a.pos;
+    if (pos < 0 || pos >= a.max_seq) {  // no cache row for it: NaN outputs
+        a.out[h * ATT_HD + d] = __builtin_nanf("");
+        return;
+    }
+    const int nch = (pos + ATT_CH) / ATT_CH;
+    float m = -INFINITY;
+    if (d < nch) {
+        msh[d] = ml0.x;
+        lsh[d] = ml0.y;
+        m = ml0.x;
+    }
+    for (int c = d + ATT_HD; c < nch; c += ATT_HD) {
+        const float2 v = *reinterpret_cast<const float2 *>(ml + 2 * c);
+        msh[c] = v.x;
+        lsh[c] = v.y;
+        m = fmaxf(m, v.x);
+    }
+    // M: the max of the m_c (a max is the same in any order)
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    if (lane == 0) mred[d >> 6] = m;
+    __syncthreads();
+    const float M = fmaxf(mred[0], mred[1]);
+    const bool fin = __builtin_isfinite(M);
+    for (int c = d; c < nch; c += ATT_HD) {
+        const float mc = msh[c];
+        wsh[c] = (fin && mc > -INFINITY) ? exp256(mc - M) : 0.0f;
+    }
+    __syncthreads();
+    float L = 0.0f, O = 0.0f;
+    for (int c0 = 0; c0 < nch; c0 += 16) {
+        float nb[16];
+        const bool more = c0 + 16 < nch;  // uniform
+        if (more) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) nb[i] = po[(size_t)min(c0 + 16 + i, nch - 1) * ATT_HD];
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            if (c0 + i < nch) {  // uniform
+                const float w = wsh[c0 + i];
+                L = fmaf(w, lsh[c0 + i], L);
+                O = fmaf(w, ob[i], O);
+            }
+        }
+        if (more) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) ob[i] = nb[i];
+        }
+    }
+    const bool ok = L > 0.0f && __builtin_isfinite(L);
+    a.out[h * ATT_HD + d] = ok ? O * (1.0f / L) : 0.0f;
 }
 
 // B: softmax (text_layer.cpp:436-535) and the value-weighted sum
@@ -351,6 +529,38 @@ __global__ __launch_bounds__(PV_THREADS) void attn_softmax_pv_kernel(AttnArgs a)
     __shared__ float hmax[4], hinv[4];
     const int kvh = blockIdx.x, db = blockIdx.y;
     const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63;
+    const uint16_t *vc = a.v_cache + ((size_t)a.layer * a.kv_heads + kvh) * S * ATT_HD + db * PV_D;
+
+    // ---- entry loads, in order of use, all issued before `pos` is known
+    // (their latency overlaps its own). Every load is unconditional, with
+    // indices clamped into the buffers, so no wait depends on which were
+    // issued; values past the context are masked once pos is known.
+    // chunk maxima: wave hh < kvm, lane c (one pass covers 4096 positions)
+    const int wh = min(wid, kvm - 1);
+    const float cm = a.cmax[(kvh * kvm + wh) * a.max_chunks + min(lane, a.max_chunks - 1)];
+    // scores: thread tid holds positions 4*(tid + PV_THREADS*k) + 0..3
+    float4 sreg[3][PV_SREG];
+#pragma unroll
+    for (int hh = 0; hh < 3; ++hh) {
+        const float4 *sc = reinterpret_cast<const float4 *>(a.scores + (size_t)(kvh * kvm + min(hh, kvm - 1)) * S);
+#pragma unroll
+        for (int k = 0; k < PV_SREG; ++k) sreg[hh][k] = sc[min(tid + PV_THREADS * k, S / 4 - 1)];
+    }
+    // V chunk loads: item -> (position t, 8-dim segment sg), the two segments of
+    // a row on adjacent lanes (a wave load covers 32 rows x 32 bytes); rows
+    // clamped into the cache (rows past pos are zeroed when stored)
+    u32x4 vr[PV_ITEMS];
+    auto load_chunk = [&](int t0) {
+#pragma unroll
+        for (int it = 0; it < PV_ITEMS; ++it) {
+            const int item = it * PV_THREADS + tid, sg = item & 1, t = t0 + (item >> 1);
+            vr[it] = *reinterpret_cast<const u32x4 *>(vc + (size_t)min(t, S - 1) * ATT_HD + sg * 8);
+        }
+    };
+    __builtin_amdgcn_sched_barrier(0);
+    load_chunk(0);
+    __builtin_amdgcn_sched_barrier(0);
+
     const int pos = *a.pos;
     if (pos < 0 || pos >= S) {  // no cache row for it: NaN outputs
         if (wid == 0 && (lane >> 4) < kvm)
@@ -360,32 +570,7 @@ __global__ __launch_bounds__(PV_THREADS) void attn_softmax_pv_kernel(AttnArgs a)
     const int n = pos + 1;
     const int nb = n & ~7;
     const int nch = (n + ATT_CH - 1) / ATT_CH;
-    const uint16_t *vc = a.v_cache + ((size_t)a.layer * a.kv_heads + kvh) * S * ATT_HD + db * PV_D;
-
-    // ---- entry loads, in order of use. Every load is unconditional (indices
-    // clamped into the buffers), so no wait depends on which were issued.
-    // chunk maxima: wave hh < kvm, lanes c < nch (one pass covers 4096 positions)
-    const int wh = min(wid, kvm - 1);
-    const float cm = a.cmax[(kvh * kvm + wh) * a.max_chunks + min(lane, nch - 1)];
-    // scores: thread tid holds positions 4*(tid + PV_THREADS*k) + 0..3
     const int kreg = min(PV_SREG, (n + 4 * PV_THREADS - 1) / (4 * PV_THREADS));  // uniform
-    float4 sreg[3][PV_SREG];
-#pragma unroll
-    for (int hh = 0; hh < 3; ++hh) {
-        const float4 *sc = reinterpret_cast<const float4 *>(a.scores + (size_t)(kvh * kvm + min(hh, kvm - 1)) * S);
-#pragma unroll
-        for (int k = 0; k < PV_SREG; ++k) sreg[hh][k] = sc[min(tid + PV_THREADS * k, S / 4 - 1)];
-    }
-    // V chunk loads: item -> (position t, 8-dim segment sg), the two segments of
-    // a row on adjacent lanes (a wave load covers 32 rows x 32 bytes)
-    u32x4 vr[PV_ITEMS];
-    auto load_chunk = [&](int t0) {
-#pragma unroll
-        for (int it = 0; it < PV_ITEMS; ++it) {
-            const int item = it * PV_THREADS + tid, sg = item & 1, t = t0 + (item >> 1);
-            vr[it] = *reinterpret_cast<const u32x4 *>(vc + (size_t)min(t, n - 1) * ATT_HD + sg * 8);
-        }
-    };
     // rows past pos are stored as zeros (their steps then add exact +0, even
     // where the row at pos holds an infinity)
     auto store_chunk = [&](int t0) {
@@ -400,14 +585,11 @@ __global__ __launch_bounds__(PV_THREADS) void attn_softmax_pv_kernel(AttnArgs a)
                 vt[(sg * 8 + i) * PV_RS + t] = h2f((uint16_t)(w[i >> 1] >> (16 * (i & 1))));
         }
     };
-    __builtin_amdgcn_sched_barrier(0);
-    load_chunk(0);
-    __builtin_amdgcn_sched_barrier(0);
 
     // ---- M per head from the chunk maxima (beyond one pass: loop)
     if (wid < kvm) {
         const float *cmh = a.cmax + (kvh * kvm + wid) * a.max_chunks;
-        float m = cm;  // loaded for head wh == wid
+        float m = lane < nch ? cm : -INFINITY;  // loaded for head wh == wid
         for (int c = lane + 64; c < nch; c += 64) m = fmaxf(m, cmh[c]);
 #pragma unroll
         for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
@@ -596,7 +778,15 @@ hipError_t launch_attention(const AttnArgs &a, hipStream_t st) {
         return hipErrorInvalidValue;
     const size_t lds = attention_lds_bytes(a.heads, a.kv_heads, a.max_seq);
     if (lds > kAttnMaxLds) return hipErrorInvalidValue;
-    attn_scores_kernel<<<dim3(a.kv_heads, a.max_chunks), ATT_THREADS, 0, st>>>(a);
+    if (a.order == 1) {  // chunked order
+        if (!a.part_o || !a.part_ml || a.max_chunks > ATT_MAX_CHUNKS) return hipErrorInvalidValue;
+        attn_scores_kernel<true><<<dim3(a.kv_heads, a.max_chunks), ATT_THREADS, 0, st>>>(a);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        attn_combine_kernel<<<a.heads, ATT_HD, 0, st>>>(a);
+        return hipGetLastError();
+    }
+    attn_scores_kernel<false><<<dim3(a.kv_heads, a.max_chunks), ATT_THREADS, 0, st>>>(a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     static int lds_set = 0;  // raise the dynamic LDS limit once per process

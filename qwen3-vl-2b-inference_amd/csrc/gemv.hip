@@ -21,6 +21,9 @@
 //     ascending group order, exactly as the reference's scalar / AVX code.
 #include <float.h>
 
+#include <mutex>
+#include <vector>
+
 #include "q3vl_device.hpp"
 #include "q3vl_kernels.hpp"
 
@@ -802,6 +805,28 @@ __global__ void swiglu_kernel(float *gate, const float *up, size_t n) {
 }
 
 // ------------------------------------------------------------------ launch
+// Launch-size cache of one kernel instantiation: the full-occupancy grid
+// (CUs x resident blocks) per (device, threads, LDS bytes).
+struct GridCache {
+    struct Entry {
+        int dev, nthr;
+        size_t lds;
+        int grid;
+    };
+    std::mutex mu;
+    std::vector<Entry> entries;
+    int find(int dev, int nthr, size_t lds) {
+        std::lock_guard<std::mutex> lk(mu);
+        for (const Entry &x : entries)
+            if (x.dev == dev && x.nthr == nthr && x.lds == lds) return x.grid;
+        return 0;
+    }
+    void put(int dev, int nthr, size_t lds, int grid) {
+        std::lock_guard<std::mutex> lk(mu);
+        entries.push_back({dev, nthr, lds, grid});
+    }
+};
+
 template <int GS, int MR, bool LANES, int R, int KC = 0, int MD = MD_RUNTIME>
 static hipError_t launch_gemv_t(const GemvArgs &a, int *grid_out, hipStream_t st) {
     const int K = a.K, Kg = K / GS;
@@ -819,15 +844,22 @@ static hipError_t launch_gemv_t(const GemvArgs &a, int *grid_out, hipStream_t st
     } else {
         for (int s = 0; s < a.nseg; ++s) ntiles += (a.seg[s].N + R - 1) / R;
     }
-    int dev = 0, cus = 0, occ = 0;
+    // CUs x resident blocks per CU of this instantiation, queried once per
+    // (device, threads, LDS bytes) and then looked up
+    static GridCache cache;
+    int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return e;
-    e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-    if (e != hipSuccess) return e;
-    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, gemv_kernel<GS, MR, LANES, R, KC, MD>, nthr, lds);
-    if (e != hipSuccess) return e;
-    if (occ < 1) occ = 1;
-    int grid = cus * occ;
+    int grid = cache.find(dev, nthr, lds);
+    if (grid <= 0) {
+        int cus = 0, occ = 0;
+        e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+        if (e != hipSuccess) return e;
+        e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, gemv_kernel<GS, MR, LANES, R, KC, MD>, nthr, lds);
+        if (e != hipSuccess) return e;
+        grid = cus * (occ < 1 ? 1 : occ);
+        cache.put(dev, nthr, lds, grid);
+    }
     if (grid > GEMV_MAX_GRID) grid = GEMV_MAX_GRID;  // argmax partials reserved per launch
     if (grid > ntiles) grid = ntiles;
     if (grid < 1) grid = 1;

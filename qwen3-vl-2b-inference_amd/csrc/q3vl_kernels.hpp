@@ -83,6 +83,8 @@ struct AttnArgs {
     uint16_t *k_cache, *v_cache;            // fp16 [layers, kv_heads, max_seq, hd]
     const int32_t *pos;                     // device: position of the new token
     float *scores, *cmax;                   // scratch [heads, max_seq], [heads, max_chunks]
+    float *part_o, *part_ml;                // chunked order: [heads, max_chunks, hd], [heads, max_chunks, 2]
+    int order;                              // 0: the reference's order, 1: chunked
     float *out;                             // [heads*hd]
     int layer, heads, kv_heads, head_dim, max_seq, max_chunks, gs;
     float eps, inv_sqrt_d;

@@ -20,7 +20,11 @@ class TextModelC(ctypes.Structure):
                 + [("eps", ctypes.c_float)]
                 + [(n, _vp) for pair in FIELD_ORDER for n in pair]
                 + [(n, _vp) for n in LINEAR_W] + [(n, _vp) for n in LINEAR_S]
-                + [("rope_cos", _vp), ("rope_sin", _vp)])
+                + [("rope_cos", _vp), ("rope_sin", _vp)]
+                + [("attn_order", ctypes.c_int)])
+
+ATTN_REFERENCE = 0  # Q3VL_ATTN_REFERENCE
+ATTN_CHUNKED = 1    # Q3VL_ATTN_CHUNKED
 
 
 def make_struct(dims: dict, ptr) -> TextModelC:
@@ -34,6 +38,7 @@ def make_struct(dims: dict, ptr) -> TextModelC:
             setattr(s, n, ptr(n))
     for n in LINEAR_W + LINEAR_S + ["rope_cos", "rope_sin"]:
         setattr(s, n, ptr(n))
+    s.attn_order = int(dims.get("attn_order", ATTN_REFERENCE))
     return s
 
 

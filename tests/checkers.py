@@ -93,14 +93,16 @@ class Oracle:
         L.orc_quantize_groupwise(_p(x), x.size, group, _p(q), _p(s))
         return q, s
 
-    def decode_step(self, dims, arrays, k_cache, v_cache, token, pos, kv_fp16=True):
-        """Returns (next_id, logits); updates the caches at pos in place."""
+    def decode_step(self, dims, arrays, k_cache, v_cache, token, pos, kv_fp16=True, chunked=False):
+        """Returns (next_id, logits); updates the caches at pos in place.
+        chunked: the chunked attention order (Q3VL_ATTN_CHUNKED)."""
         L = self.lib
         L.orc_decode_step.restype = ctypes.c_int32
         L.orc_decode_step.argtypes = [_vp, _vp, _vp, ctypes.c_int, ctypes.c_int32, _sz, _vp]
         st = _model_struct(dims, arrays)
         logits = np.zeros(dims["vocab"], np.float32)
-        nid = L.orc_decode_step(ctypes.byref(st), _p(k_cache), _p(v_cache), int(kv_fp16), token,
+        flags = (1 if kv_fp16 else 0) | (2 if chunked else 0)
+        nid = L.orc_decode_step(ctypes.byref(st), _p(k_cache), _p(v_cache), flags, token,
                                 pos, _p(logits))
         return int(nid), logits
 
@@ -142,6 +144,18 @@ class Oracle:
         L.orc_attention(_p(np.ascontiguousarray(q, np.float32)), _p(np.ascontiguousarray(kc, np.float32)),
                         _p(np.ascontiguousarray(vc, np.float32)), heads, kv_heads, hd, max_seq, pos,
                         _p(att), _p(out))
+        return out
+
+    def attention_chunked(self, q, kc, vc, heads, kv_heads, hd, max_seq, pos):
+        """The chunked attention order (Q3VL_ATTN_CHUNKED) of one layer."""
+        L = self.lib
+        L.orc_attention_chunked.argtypes = [_vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _vp, _vp]
+        att = np.zeros(pos + 1, np.float32)
+        out = np.zeros(heads * hd, np.float32)
+        L.orc_attention_chunked(_p(np.ascontiguousarray(q, np.float32)),
+                                _p(np.ascontiguousarray(kc, np.float32)),
+                                _p(np.ascontiguousarray(vc, np.float32)), heads, kv_heads, hd,
+                                max_seq, pos, _p(att), _p(out))
         return out
 
     def argmax_rows(self, logits):

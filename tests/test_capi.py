@@ -15,7 +15,7 @@ def test_library_exports_every_declared_function():
     assert len(names) >= 15
     missing = [n for n in names if not hasattr(lib, n)]
     assert not missing, missing
-    assert lib.q3vl_abi_version() == 2
+    assert lib.q3vl_abi_version() == 3
 
 
 def test_linear_dropin_exports_cpp_linear():

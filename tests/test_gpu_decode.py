@@ -50,7 +50,7 @@ class Stepper:
                             self.ws)
         torch.cuda.synchronize()
         nid, lo = self.orc.decode_step(self.dims, self.m, self.ko, self.vo, self.token, self.p,
-                                       kv_fp16=True)
+                                       kv_fp16=True, chunked=self.dims.get("attn_order", 0) == 1)
         lg = self.logits.cpu().numpy()
         tag = f"pos={self.p} token={self.token}"
         np.testing.assert_array_equal(lg.view(np.uint32), lo.view(np.uint32), err_msg=tag)
@@ -133,3 +133,60 @@ def test_decode_full_config_step(dev, orc):
     s = Stepper(dev, orc, dims, seed=60, ctx=1024, token=151000)
     print("full-size decode step: stepping", flush=True)
     s.step()
+
+
+# ---------------------------------------------- the chunked attention order
+# Q3VL_ATTN_CHUNKED (no counterpart in the reference): checked bit for bit
+# against the oracle's restatement of that order (orc_attention_chunked),
+# whose own distance from the reference order is pinned on the CPU.
+CHUNKED = 1
+
+
+@pytest.mark.parametrize("pos", [0, 7, 63, 64, 65, 127, 255])
+def test_decode_chunked_edge_positions(dev, orc, pos):
+    dims = dict(SMALL, layers=1, attn_order=CHUNKED)
+    Stepper(dev, orc, dims, seed=130 + pos, ctx=pos, token=pos % 4096).step()
+
+
+def test_decode_chunked_chained_steps(dev, orc):
+    s = Stepper(dev, orc, dict(SMALL, attn_order=CHUNKED), seed=121, ctx=126, token=7)
+    for _ in range(4):  # crosses the chunk boundary at 128
+        s.step()
+
+
+@pytest.mark.parametrize("pos", [1000, 2100])
+def test_decode_chunked_stale_rows_past_the_context(dev, orc, pos):
+    dims = dict(SMALL, layers=1, max_seq=2304, attn_order=CHUNKED)
+    Stepper(dev, orc, dims, seed=145, ctx=pos, token=5, stale_nan=True).step()
+
+
+def test_decode_chunked_three_query_heads_per_kv_head(dev, orc):
+    dims = dict(SMALL, layers=1, heads=24, kv_heads=8, hidden=3072, inter=1024, attn_order=CHUNKED)
+    Stepper(dev, orc, dims, seed=150, ctx=200, token=3).step()
+
+
+def test_decode_chunked_full_config_step(dev, orc):
+    print("full-size chunked decode step: building model", flush=True)
+    dims = dict(QWEN3VL_2B, max_seq=1088, attn_order=CHUNKED)
+    s = Stepper(dev, orc, dims, seed=160, ctx=1024, token=151000)
+    print("full-size chunked decode step: stepping", flush=True)
+    s.step()
+
+
+def test_decode_chunked_position_out_of_range(dev):
+    """*pos = max_seq: caches untouched, logits NaN, as in the reference order."""
+    torch, qm = dev
+    dims = dict(SMALL, layers=1, max_seq=256, attn_order=CHUNKED)
+    m = make_text_model(170, dims)
+    k16, v16 = make_kv_cache(171, dims, 256)
+    model = qm.DeviceTextModel(dims, m)
+    kd = torch.from_numpy(k16.view(np.int16).copy()).cuda()
+    vd = torch.from_numpy(v16.view(np.int16).copy()).cuda()
+    tok = torch.tensor([9], dtype=torch.int32, device="cuda")
+    pos = torch.tensor([256], dtype=torch.int32, device="cuda")
+    logits = torch.zeros(dims["vocab"], dtype=torch.float32, device="cuda")
+    qm.decode_step(model, kd, vd, tok, pos, logits, qm.alloc_decode_workspace(model))
+    torch.cuda.synchronize()
+    assert torch.isnan(logits).all()
+    np.testing.assert_array_equal(kd.cpu().numpy(), k16.view(np.int16))
+    np.testing.assert_array_equal(vd.cpu().numpy(), v16.view(np.int16))
