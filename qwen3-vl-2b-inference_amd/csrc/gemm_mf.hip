@@ -15,24 +15,32 @@
 // Data movement, from what this hardware measured (per CU: LDS reads about
 // 110 B/clk, L1 about 62 B/clk, one 32x32x16 MFMA about 34 cycles; the
 // epilogue's two fp32 operations per output and group cost as much VALU time
-// as the MFMAs, so the kernel is VALU-bound and the operand traffic is split
-// between the two paths):
+// as the MFMAs). Per-phase cycle counts showed the waves stalled at issuing
+// their global loads: the vector memory path, not the MFMAs or the VALU,
+// was the limit, so every operand is loaded once per block and staged into
+// LDS, and the weight scales, which a per-group load fetched one cache line
+// per weight row at a time, come in tiles of several groups:
 // * A: the quantizer writes q in fragment order -- per 32-row m-tile t and
 //   group g a 4 KB chunk [slice s][lane l][8 halves] holding
-//   q[32t + l%32][64g + 32(l/32) + 8s + j] -- so each wave loads its A
-//   fragments straight from L1/L2 with one coalesced 1 KB read per slice.
-//   Its scales come in the same order: [t][g][l/32][16] holds a_s of rows
-//   32t + 8(e/4) + 4(l/32) + e%4, the rows a lane's 16 accumulators hold.
+//   q[32t + l%32][64g + 32(l/32) + 8s + j]. Wave w loads slice w of each of
+//   the block's m-tiles (one coalesced 1 KB read each) and stores it to LDS
+//   unchanged; every wave then reads its fragments with one ds_read_b128 per
+//   slice and m-tile. The a_s come in the matching order: [t][g][l/32][16]
+//   holds a_s of rows 32t + 8(e/4) + 4(l/32) + e%4, the rows a lane's 16
+//   accumulators hold.
 // * B: the block loads its weight rows (64 bytes per row and group) once,
 //   widens them to fp16 (0x64xx exponent trick) and stores them in LDS in the
 //   same fragment order, two buffers deep, so every wave reads its B
 //   fragments with one ds_read_b128 per slice and n-tile. The 16-byte slots
 //   are swizzled (slot ^ 4*(s/2) ^ 8*(l/32)) so that the writers' and the
 //   readers' 16-lane passes each hit 16 distinct bank groups.
+// * w_s: every SG groups (8, or 4 where three blocks' LDS must fit) the
+//   block loads the next SG scales of each of its weight rows, 2 threads per
+//   row, contiguous 4 SG bytes per row, into a second LDS tile slot.
 // * The k order inside a group: slice s of lane half h covers k = 32h + 8s +
 //   j; A and B use the same map, so each MFMA pairs matching k and the four
 //   slices cover the group's 64 k once.
-// * Block: 4 waves in WM x (4/WM), wave tile (32 TM) x (32 TN); two or three
+// * Block: 4 waves in WM x (4/WM), wave tile (32 TM) x (32 TN); two to four
 //   blocks share a CU, so one block's epilogue overlaps another's MFMAs and
 //   its loads another's waits. One barrier per group (an LDS-only fence).
 //   WM = 1 serves M <= 32 (one m-tile): all four waves take output columns.
@@ -54,14 +62,19 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 // quantize_rows_kernel computes it (16 lanes per group: lane i runs the FMA
 // chain over x[16t + i], then the fixed tree), writing q as fp16 in the
 // fragment order above and a_s in its fragment order. Rows M .. 32*Mt-1 are
-// written as zeros. One row and 16 groups per 256-thread block.
+// written as zeros. A 256-thread block takes 8 consecutive rows of an m-tile
+// and 2 groups (16 lanes per row and group): a 128-byte line of the fragment
+// order holds 16 bytes of each of 8 consecutive rows, so every line is
+// written whole by one block (rows of a line spread over blocks on several
+// XCDs would leave partial lines in several L2s).
 __global__ __launch_bounds__(256) void quantize_frag_kernel(const float *__restrict__ A,
                                                             _Float16 *__restrict__ qf,
                                                             float *__restrict__ asf, int M, int K) {
     const int Kg = K / 64;
     const int lane16 = threadIdx.x & 15;
-    const int g = blockIdx.x * 16 + (threadIdx.x >> 4);
-    const int m = blockIdx.y;
+    const int pair = threadIdx.x >> 4;  // row pair & 7, group pair >> 3 of the block
+    const int g = blockIdx.x * 2 + (pair >> 3);
+    const int m = blockIdx.y * 8 + (pair & 7);
     if (g >= Kg) return;  // whole 16-lane groups leave together
     const bool real = m < M;
     const float *x = A + (size_t)(real ? m : 0) * K + (size_t)g * 64;
@@ -97,7 +110,7 @@ hipError_t launch_quantize_frag(const float *A, _Float16 *qf, float *asf, int M,
                                 hipStream_t st) {
     if (K % 64 != 0 || M < 1) return hipErrorInvalidValue;
     const int Mt = (M + 31) / 32;
-    dim3 grid((K / 64 + 15) / 16, Mt * 32);
+    dim3 grid((K / 64 + 1) / 2, Mt * 4);
     quantize_frag_kernel<<<grid, 256, 0, st>>>(A, qf, asf, M, K);
     return hipGetLastError();
 }
@@ -119,14 +132,20 @@ __device__ __forceinline__ int bslot(int s, int l) {
     return s * 64 + (l ^ ((s & 2) << 1) ^ ((l & 32) >> 2));
 }
 
-// BPC: blocks per CU the register budget is sized for. D: groups whose global
-// loads are in flight (a ring of D register sets). Loads return in order, so
-// every operand of a group -- A fragments, raw B, a_s, w_s -- is issued at the
-// same distance D ahead. A ring value is consumed (A by the MFMAs, the rest
-// by the staging into LDS) before its slot is reloaded; a value copied out of
-// the ring into other registers would make each reload wait for that copy's
-// load, which the in-order return turns into a wait for the whole ring.
-template <int TM, int TN, bool SWIGLU, int D, int BPC, int WM = 2>
+// BPC: blocks per CU the register budget is sized for. D: groups whose
+// global loads are in flight (a ring of D register sets; D divides kWsTile).
+// AL: the block's A fragments are loaded once per block (each wave a share)
+// and staged into LDS beside B, instead of each wave loading its own from
+// L1/L2. The weight scales come as tiles of kWsTile groups: per weight row
+// 4 * kWsTile contiguous bytes in one or two 16-byte loads, where a per-group
+// load would touch a cache line of every row each group. A ring value is
+// consumed by the staging (or, for A without AL, by the MFMAs) before its
+// slot is reloaded; a value copied out of the ring into other registers
+// would make each reload wait for that copy's load, which the in-order
+// return turns into a wait for the whole ring. SG: groups per w_s tile (a
+// power of two, at most kWsTile; K must be a multiple of 64 kWsTile).
+constexpr int kWsTile = 8;
+template <int TM, int TN, bool SWIGLU, int D, int BPC, int WM = 2, bool AL = true, int SG = kWsTile>
 __global__ __launch_bounds__(256, BPC) void gemm_mf_kernel(GemmMfArgs a) {
     constexpr int WN = 4 / WM;              // waves along N
     constexpr int MTB = WM * TM;            // m-tiles of the block
@@ -134,13 +153,20 @@ __global__ __launch_bounds__(256, BPC) void gemm_mf_kernel(GemmMfArgs a) {
     constexpr int NT = BN / 32;             // n-tiles in the B buffer
     constexpr int BCH = BN * 4 / 256;       // 16-byte weight chunks per thread and group
     constexpr int BBUF = NT * 4 * 64 * 16;  // bytes of one B buffer
+    constexpr int ABUF = AL ? MTB * 4 * 1024 : 0;  // bytes of one A buffer
+    constexpr int WB = SG * 4 / 2;          // bytes of a row's tile that one thread loads (2 per row)
+    constexpr int WCH = (2 * BN + 255) / 256;  // w_s tile chunks per thread
+    static_assert(SG >= 2 && SG <= kWsTile && (SG & (SG - 1)) == 0 && kWsTile % SG == 0, "w_s tile");
     static_assert(!SWIGLU || (TN == 2 && WM == 2), "SwiGLU pairs one gate and one up n-tile per wave");
     static_assert(WM == 1 || WM == 2, "2 x 2 or 1 x 4 waves");
+    static_assert(D >= 2 && SG % D == 0, "group g+1 is staged from loads issued a group earlier");
     extern __shared__ __align__(16) unsigned char smem[];
-    float *asl = reinterpret_cast<float *>(smem + 2 * BBUF);  // [3][MTB m-tiles][32]
-    float *wsl = asl + 3 * 32 * MTB;                            // [3][BN]
+    unsigned char *Asm = smem + 2 * BBUF;                        // [2][MTB][4 slices][64 lanes][16 B]
+    float *asl = reinterpret_cast<float *>(Asm + 2 * ABUF);      // [2][MTB m-tiles][32]
+    float *wsl = asl + 2 * 32 * MTB;                              // [2 tiles][SG][BN]
 
-    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
     const int wm = wid % WM, wn = wid / WM;
     const int M = a.M, N = a.N, K = a.K, Kg = K / 64, Mt = a.Mt;
     const int ncols = SWIGLU ? BN / 2 : BN;  // output columns of the block
@@ -174,12 +200,16 @@ __global__ __launch_bounds__(256, BPC) void gemm_mf_kernel(GemmMfArgs a) {
     const __amdgpu_buffer_rsrc_t rS1 =
         __builtin_amdgcn_make_buffer_rsrc((void *)(SWIGLU ? a.S1 : a.S0), 0, N * Kg * 4, kRsrcWord3);
 
-    // ---- A fragment offsets of this wave (m-tiles clamped into the buffer)
-    int aoff[TM];
+    // ---- A: with AL, wave w loads slice w of each of the block's MTB
+    // m-tiles (1 KB each, m-tiles clamped into the buffer), in the LDS layout
+    // of the fragments [m-tile][slice][lane][16 B]; without AL, each wave
+    // loads the four slices of its own TM m-tiles
+    constexpr int AU = AL ? MTB : TM;  // A ring entries per thread (AL: 1 slice; else 4)
+    int aoff[AU];
 #pragma unroll
-    for (int i = 0; i < TM; ++i) {
-        const int mt = min(mt0 + wm * TM + i, Mt - 1);
-        aoff[i] = (mt * Kg * 256 + lane) * 16;
+    for (int i = 0; i < AU; ++i) {
+        const int mt = min(mt0 + (AL ? i : wm * TM + i), Mt - 1);
+        aoff[i] = ((mt * Kg * 4 + (AL ? wid : 0)) * 64 + lane) * 16;
     }
     // ---- B staging: chunk q = tid + 256 i -> row q / 4, 16-byte piece q % 4
     // (under SWIGLU the chunks with i >= BCH / 2 are the up rows)
@@ -195,20 +225,34 @@ __global__ __launch_bounds__(256, BPC) void gemm_mf_kernel(GemmMfArgs a) {
         bdst0[i] = (nt * 256 + bslot(s0, l)) * 16;
         bdst1[i] = (nt * 256 + bslot(s0 + 1, l)) * 16;
     }
-    // ---- a_s staging: threads < 8 MTB copy one float4 each (MTB m-tiles of
-    // 32 scales per group)
-    int as_off = 0, as_dst = 0;
-    const bool as_thr = tid < 8 * MTB;
-    if (as_thr) {
-        const int i = tid >> 3, part = tid & 7;  // m-tile i of the block, 16 B piece
+    // ---- a_s staging: 8 MTB threads copy one float4 each (MTB m-tiles of
+    // 32 scales per group); every thread loads and stores, the others a
+    // duplicate of thread tid % (8 MTB) -- the same value to the same place,
+    // so no path leaves a scale load outstanding into the loop
+    int as_off, as_dst;
+    {
+        const int q = tid % (8 * MTB);
+        const int i = q >> 3, part = q & 7;  // m-tile i of the block, 16 B piece
         const int mt = min(mt0 + i, Mt - 1);
         as_off = (mt * Kg * 32 + 4 * part) * 4;
         as_dst = i * 32 + 4 * part;
     }
-    // ---- w_s staging: thread t < BN copies the scale of B row t each group
-    const bool ws_thr = tid < BN;
-    const bool ws_up = SWIGLU && tid >= BN / 2;
-    const int ws_off = min(n0 + (ws_up ? tid - BN / 2 : (ws_thr ? tid : 0)), N - 1) * Kg * 4;
+    // ---- w_s tiles: chunk q = tid + 256 c -> B row (q / 2) % BN, groups
+    // (SG / 2) (q % 2) .. of the tile (chunks past the rows duplicate a row:
+    // the same values to the same place). Under SWIGLU rows >= BN / 2 are the
+    // up rows, taken by whole waves, so the resource stays scalar.
+    static_assert(!SWIGLU || BN == 128 || BN == 256, "SwiGLU w_s chunks split at a wave");
+    int wso[WCH], wsr[WCH], wsh[WCH];
+    bool wsu[WCH];
+#pragma unroll
+    for (int c = 0; c < WCH; ++c) {
+        const int q = tid + 256 * c, row = (q >> 1) % BN;
+        wsu[c] = SWIGLU && __builtin_amdgcn_readfirstlane(row) >= BN / 2;  // whole waves
+        wsr[c] = row;
+        wsh[c] = q & 1;
+        const int nrow = min(n0 + (wsu[c] ? row - BN / 2 : row), N - 1);
+        wso[c] = (nrow * Kg + (SG / 2) * (q & 1)) * 4;
+    }
     // ---- this lane's output columns (n-tile bt[j] of the B buffer)
     int bt[TN];
     int ncol[TN];
@@ -225,33 +269,58 @@ __global__ __launch_bounds__(256, BPC) void gemm_mf_kernel(GemmMfArgs a) {
     const int h = lane >> 5;
 
     // ---- the ring of in-flight loads: group g's operands in slot g % D
+    u32x4 araw[D][AU][AL ? 1 : 4];
     u32x4 braw[D][BCH];
     float4 asraw[D];
-    u32x4 af[D][TM][4];
-    float wsraw[D];
+    typedef float wsv_t __attribute__((ext_vector_type(SG / 2)));
+    wsv_t wst[WCH];  // the next w_s tile
     auto load_group = [&](int sl, int g) {
 #pragma unroll
-        for (int i = 0; i < TM; ++i)
+        for (int i = 0; i < AU; ++i)
 #pragma unroll
-            for (int s = 0; s < 4; ++s)
-                af[sl][i][s] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                             rA, aoff[i], g * 4096 + s * 1024, 0));
+            for (int s = 0; s < (AL ? 1 : 4); ++s)
+                araw[sl][i][s] = __builtin_bit_cast(
+                    u32x4, __builtin_amdgcn_raw_buffer_load_b128(rA, aoff[i], g * 4096 + s * 1024, 0));
 #pragma unroll
         for (int i = 0; i < BCH; ++i) {
             const bool up = SWIGLU && i >= BCH / 2;
             braw[sl][i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
                                                         up ? rW1 : rW0, boff[i], 64 * g, 0));
         }
-        // (threads past the MTB m-tiles read scales at offset 128 g of the
-        // buffer and discard them: the scalar offset stays uniform)
         asraw[sl] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rAS, as_off, 128 * g, 0));
-        wsraw[sl] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                                  ws_up ? rS1 : rS0, ws_off, 4 * g, 0));
     };
-    // group g's B (ring slot sl) goes to B buffer g % 2, its scales to the
-    // a_s and w_s slots g % 3 (every ring value is consumed here, before its
-    // slot is reloaded, so a reload never waits for the load it replaces)
+    // w_s tile of groups g .. g + SG - 1
+    auto load_ws = [&](int g) {
+#pragma unroll
+        for (int c = 0; c < WCH; ++c) {
+            if constexpr (WB == 16)
+                wst[c] = __builtin_bit_cast(wsv_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                                       wsu[c] ? rS1 : rS0, wso[c], 4 * g, 0));
+            else if constexpr (WB == 8)
+                wst[c] = __builtin_bit_cast(wsv_t, __builtin_amdgcn_raw_buffer_load_b64(
+                                                       wsu[c] ? rS1 : rS0, wso[c], 4 * g, 0));
+            else
+                wst[c] = __builtin_bit_cast(wsv_t, __builtin_amdgcn_raw_buffer_load_b32(
+                                                       wsu[c] ? rS1 : rS0, wso[c], 4 * g, 0));
+        }
+    };
+    auto store_ws = [&](int g) {  // into tile slot (g / SG) % 2
+        float *slot = wsl + ((g / SG) & 1) * SG * BN;
+#pragma unroll
+        for (int c = 0; c < WCH; ++c)
+#pragma unroll
+            for (int k = 0; k < SG / 2; ++k) slot[((SG / 2) * wsh[c] + k) * BN + wsr[c]] = wst[c][k];
+    };
+    // group g (ring slot sl) goes to the A (with AL) and B buffers g % 2, its
+    // a_s to slot g % 2 (every ring value is consumed here, before its slot
+    // is reloaded, so a reload never waits for the load it replaces)
     auto stage = [&](int sl, int g) {
+        if constexpr (AL) {
+            unsigned char *As = Asm + (g & 1) * ABUF;
+#pragma unroll
+            for (int i = 0; i < MTB; ++i)
+                *reinterpret_cast<u32x4 *>(As + ((i * 4 + wid) * 64 + lane) * 16) = araw[sl][i][0];
+        }
         unsigned char *Bs = smem + (g & 1) * BBUF;
 #pragma unroll
         for (int i = 0; i < BCH; ++i) {
@@ -264,8 +333,7 @@ __global__ __launch_bounds__(256, BPC) void gemm_mf_kernel(GemmMfArgs a) {
             *reinterpret_cast<u32x4 *>(Bs + bdst0[i]) = (u32x4){w[0], w[1], w[2], w[3]};
             *reinterpret_cast<u32x4 *>(Bs + bdst1[i]) = (u32x4){w[4], w[5], w[6], w[7]};
         }
-        if (as_thr) *reinterpret_cast<float4 *>(asl + (g % 3) * 32 * MTB + as_dst) = asraw[sl];
-        if (ws_thr) wsl[(g % 3) * BN + tid] = wsraw[sl];
+        *reinterpret_cast<float4 *>(asl + (g & 1) * 32 * MTB + as_dst) = asraw[sl];
     };
 
     // one accumulator set: the MFMA -> epilogue chain of one wave is hidden
@@ -276,39 +344,56 @@ __global__ __launch_bounds__(256, BPC) void gemm_mf_kernel(GemmMfArgs a) {
 #pragma unroll
         for (int j = 0; j < TN; ++j) out[i][j] = (float16_t)(0.0f);
 
-    // ---- prologue: groups 0 .. D-1 in flight (clamped: a repeated load of
-    // the last group keeps the ring full), group 0 staged
+    // ---- prologue: w_s tile 0 and groups 0 .. D-1 in flight (clamped: a
+    // repeated load of the last group keeps the ring full), w_s tile 0 and
+    // group 0 staged
+    load_ws(0);
 #pragma unroll
     for (int j = 0; j < D; ++j) load_group(j, min(j, Kg - 1));
+    store_ws(0);
     stage(0, 0);
+    // Enter the loop with no load outstanding (vmcnt(0); group 0's data had
+    // to arrive anyway, the others were issued right behind it): the
+    // compiler's wait counts at the loop head then follow the loop's own
+    // order of loads alone, not a merge with the prologue's.
+    __builtin_amdgcn_s_waitcnt(0x0F70);
     __syncthreads();
 
-    // B fragments of group g (all four slices, issued together)
-    auto read_b = [&](half8_t (&bfr)[4][TN], int g) {
+    // The MFMAs of group g (B from LDS buffer g % 2; A from LDS buffer g % 2
+    // with AL, else from ring slot sl): the fragments of slice s + 1 are read
+    // while slice s multiplies
+    auto mfmas = [&](int g, int sl) {
+        const unsigned char *As = Asm + (g & 1) * ABUF + (wm * TM * 4 * 64 + lane) * 16;
         const unsigned char *Bs = smem + (g & 1) * BBUF;
+        half8_t afr[2][TM], bfr[2][TN];
+        auto rd = [&](int s) {
 #pragma unroll
-        for (int s = 0; s < 4; ++s)
+            for (int i = 0; i < TM; ++i)
+                afr[s & 1][i] = AL ? *reinterpret_cast<const half8_t *>(As + (i * 4 + s) * 1024)
+                                   : __builtin_bit_cast(half8_t, araw[sl][AL ? 0 : i][AL ? 0 : s]);
 #pragma unroll
             for (int j = 0; j < TN; ++j)
-                bfr[s][j] = *reinterpret_cast<const half8_t *>(Bs + (bt[j] * 256 + bslot(s, lane)) * 16);
-    };
-    auto mfmas = [&](int sl, const half8_t (&bfr)[4][TN]) {
+                bfr[s & 1][j] = *reinterpret_cast<const half8_t *>(Bs + (bt[j] * 256 + bslot(s, lane)) * 16);
+        };
+        rd(0);
 #pragma unroll
-        for (int s = 0; s < 4; ++s)
+        for (int s = 0; s < 4; ++s) {
+            if (s + 1 < 4) rd(s + 1);
 #pragma unroll
             for (int i = 0; i < TM; ++i)
 #pragma unroll
                 for (int j = 0; j < TN; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-                        __builtin_bit_cast(half8_t, af[sl][i][s]), bfr[s][j],
-                        s == 0 ? (float16_t)(0.0f) : acc[i][j], 0, 0, 0);
+                        afr[s & 1][i], bfr[s & 1][j], s == 0 ? (float16_t)(0.0f) : acc[i][j], 0, 0, 0);
+        }
     };
     // epilogue of group g, reference order: out = fma(G * a_s, w_s, out)
     auto epilogue = [&](int g) {
-        const float *as_g = asl + (g % 3) * 32 * MTB + wm * TM * 32 + h * 16;
+        const float *as_g = asl + (g & 1) * 32 * MTB + wm * TM * 32 + h * 16;
+        const float *ws_t = wsl + ((g / SG) & 1) * SG * BN + (g % SG) * BN;
         float ws_g[TN];
 #pragma unroll
-        for (int j = 0; j < TN; ++j) ws_g[j] = wsl[(g % 3) * BN + bt[j] * 32 + (lane & 31)];
+        for (int j = 0; j < TN; ++j) ws_g[j] = ws_t[bt[j] * 32 + (lane & 31)];
 #pragma unroll
         for (int i = 0; i < TM; ++i) {
             float asv[16];
@@ -327,28 +412,50 @@ __global__ __launch_bounds__(256, BPC) void gemm_mf_kernel(GemmMfArgs a) {
                     out[i][j][e] = fmaf(acc[i][j][e] * asv[e], ws_g[j], out[i][j][e]);
         }
     };
-    // group g (ring slot sl = g % D): MFMAs from B buffer g % 2, reload slot
-    // sl with group g+D, stage group g+1, the epilogue, barrier
-    auto group = [&](int sl, int g) {
-        half8_t bfr[4][TN];
-        read_b(bfr, g);
-        mfmas(sl, bfr);
-        // slot sl's A went into the MFMAs above and its B was staged one
-        // group ago, so it takes group g+D now; issued before the staging of
-        // group g+1 (slot (g+1) % D, which is slot sl itself when D = 1).
-        // Unconditional (the last group is reloaded near the end), so the
-        // compiler's count of loads in flight is the same on every path.
+    // group g = g0 + j (ring slot sl = j % D): MFMAs, reload slot sl with
+    // group g+D (and at j = 0 the w_s tile after the current one), the
+    // epilogue, stage group g+1 (slot (g+1) % D, loaded D-1 groups ago; at
+    // j = SG-1 also the w_s tile loaded SG-1 groups ago), barrier. The
+    // scheduling barriers keep that order: staging group g+1 any earlier
+    // (say beside the MFMAs) would wait for its loads sooner, instead of the
+    // MFMAs of the other blocks on the CU hiding this wave's MFMA -> epilogue
+    // dependency.
+    auto group = [&](int g0, int j) {
+        const int g = g0 + j, sl = j % D;
+        mfmas(g, sl);
+        // slot sl was consumed (staged one group ago; without AL its A just
+        // went into the MFMAs), so it takes group g+D now. Unconditional (the
+        // last group is reloaded near the end), so the compiler's count of
+        // loads in flight is the same on every path.
         load_group(sl, min(g + D, Kg - 1));
-        if (g + 1 < Kg) stage((sl + 1) % D, g + 1);
+        if (j == 0) load_ws(min(g0 + SG, Kg - SG));  // j is a compile-time constant
+        __builtin_amdgcn_sched_barrier(0);
         epilogue(g);
+        __builtin_amdgcn_sched_barrier(0);
+        // also after the last group (the buffers and slots it fills are not
+        // read again; ring and tile hold clamped reloads), so every path
+        // waits for the same loads. Buffers (g+1) % 2 were last read before
+        // the previous barrier, as were a_s slot (g+1) % 2 (by the epilogues
+        // of group g-1); w_s tile slot ((g+1) / SG) % 2 is not the one the
+        // epilogues of group g read.
+        stage((sl + 1) % D, g + 1);
+        if (j == SG - 1) store_ws(g + 1);
         // LDS-only barrier: a __syncthreads() here would also wait for every
         // global load in flight and empty the load ring at each group
         lds_barrier();
+        // nothing crosses from one group to the next: global loads hoisted
+        // over the barrier would pile up in registers across the unrolled
+        // groups
+        __builtin_amdgcn_sched_barrier(0);
     };
-    for (int g0 = 0; g0 < Kg; g0 += D) {  // unrolled by D: ring slots static
+    // unrolled by SG (Kg is a multiple of SG and SG of D): ring slots and
+    // tile steps are static, and the loop body has no exit inside (a path
+    // that left part of it would reach the loop head with other loads
+    // outstanding, and the compiler's wait counts at the head cover every
+    // path)
+    for (int g0 = 0; g0 < Kg; g0 += SG) {
 #pragma unroll
-        for (int j = 0; j < D; ++j)
-            if (g0 + j < Kg) group(j, g0 + j);  // uniform
+        for (int j = 0; j < SG; ++j) group(g0, j);
     }
 
     // ---- store
@@ -370,49 +477,43 @@ __global__ __launch_bounds__(256, BPC) void gemm_mf_kernel(GemmMfArgs a) {
     }
 }
 
-template <int TM, int TN, bool SWIGLU, int D, int BPC, int WM = 2>
+template <int TM, int TN, bool SWIGLU, int D, int BPC, int WM = 2, bool AL = true, int SG = kWsTile>
 static hipError_t launch_mf(const GemmMfArgs &a, hipStream_t st) {
     constexpr int BN = 32 * (4 / WM) * TN, MTB = WM * TM;
     const int ncols = SWIGLU ? BN / 2 : BN;
     const int tiles = ((a.N + ncols - 1) / ncols) * ((a.Mt + MTB - 1) / MTB);
     const int grid = 8 * ((tiles + 7) / 8);  // see the tile order in the kernel
-    const size_t lds = 2 * (BN / 32) * 4 * 64 * 16 + 3 * 32 * MTB * 4 + 3 * BN * 4;
-    gemm_mf_kernel<TM, TN, SWIGLU, D, BPC, WM><<<grid, 256, lds, st>>>(a);
+    const size_t lds = 2 * (BN / 32) * 4 * 64 * 16 + (AL ? 2 * MTB * 4096 : 0) + 2 * 32 * MTB * 4 + 2 * SG * BN * 4;
+    gemm_mf_kernel<TM, TN, SWIGLU, D, BPC, WM, AL, SG><<<grid, 256, lds, st>>>(a);
     return hipGetLastError();
 }
 
 // Where this kernel serves (the caller quantizes in fragment order for it)
 // and with which tiles, from timings of the prefill, vision and lm_head
-// shapes on MI355X. SwiGLU: always; 64 x (64 gate + 64 up) tiles at 3 blocks
-// per CU while the grid fits one round of the device, else 128-row tiles.
-// Plain: while 64 x 64 tiles give every CU at least two blocks; one m-tile
-// (M <= 32, e.g. the lm_head over a few rows) takes 32 x 128 tiles of 1 x 4
-// waves, more m-tiles 128 x 64 tiles once those give every CU about two.
-// Long-K shapes with fewer tiles (down_proj at M = 512, the vision fc2 and
-// merger at K = 4096) run faster on gemm_g64_kernel, whose A tiles go
-// through LDS.
+// shapes on MI355X: every group-64 product whose K is a whole number of w_s
+// tiles (K % 512 == 0). SwiGLU: 64 x (64 gate + 64 up) tiles at 3 blocks per
+// CU (4-group w_s tiles, so three blocks' LDS fit) while the grid fits one
+// round of the device, else 128-row tiles at 2 blocks per CU. Plain: one
+// m-tile (M <= 32, e.g. the lm_head over a few rows) takes 32 x 128 tiles of
+// 1 x 4 waves; more m-tiles take 64 x 64 tiles at 4 blocks per CU.
 static long mf_blocks(const GemmMfArgs &a, int tm, int ncols) {
     return (long)((a.N + ncols - 1) / ncols) * ((a.Mt + 2 * tm - 1) / (2 * tm));
 }
 
 bool gemm_mf_serves(int M, int N, int K, bool swiglu, int cus) {
-    if (K % 64 != 0 || K < 64 || M < 1 || N < 1) return false;
-    if (swiglu) return true;
-    GemmMfArgs a{};
-    a.Mt = (M + 31) / 32;
-    a.N = N;
-    return mf_blocks(a, 1, 64) >= 2L * cus;
+    (void)swiglu;
+    (void)cus;
+    return K % (64 * kWsTile) == 0 && K > 0 && M >= 1 && N >= 1;  // whole w_s tiles
 }
 
 hipError_t launch_gemm_mf(const GemmMfArgs &a, bool swiglu, int cus, hipStream_t st) {
-    if (a.K % 64 != 0 || a.K < 64 || a.M < 1 || a.N < 1) return hipErrorInvalidValue;
+    if (a.K % (64 * kWsTile) != 0 || a.K <= 0 || a.M < 1 || a.N < 1) return hipErrorInvalidValue;
     if (swiglu) {
-        if (mf_blocks(a, 1, 64) <= 3L * cus) return launch_mf<1, 2, true, 1, 3>(a, st);
-        return launch_mf<2, 2, true, 1, 2>(a, st);
+        if (mf_blocks(a, 1, 64) <= 3L * cus) return launch_mf<1, 2, true, 2, 3, 2, true, 4>(a, st);
+        return launch_mf<2, 2, true, 2, 2, 2, true, 8>(a, st);
     }
-    if (a.Mt == 1) return launch_mf<1, 1, false, 2, 3, 1>(a, st);
-    if (4 * mf_blocks(a, 2, 64) >= 7L * cus) return launch_mf<2, 1, false, 2, 2>(a, st);
-    return launch_mf<1, 1, false, 2, 2>(a, st);
+    if (a.Mt == 1) return launch_mf<1, 1, false, 2, 3, 1, true, 8>(a, st);
+    return launch_mf<1, 1, false, 2, 4, 2, true, 8>(a, st);
 }
 
 }  // namespace q3vl

@@ -121,19 +121,24 @@ def test_gemm_parity(orc, M, N, K, gs):
 
 
 @pytest.mark.parametrize("M,N,K", [(9, 128, 1024), (100, 200, 2048), (130, 260, 1024), (7, 65600, 1024),
-                                   (17, 33000, 1024),
+                                   (17, 33000, 1024), (64, 512, 512), (300, 700, 1536), (33, 4100, 1536),
                                    (784, 3072, 1024), (196, 2048, 4096), (512, 8192, 1024),
                                    (513, 8200, 1024), (512, 2048, 6144), (1030, 8200, 128),
                                    (1024, 8192, 256)])
 def test_gemm_group64_tiles_parity(orc, M, N, K):
-    """The group-64 MFMA GEMM at each of its tile variants (64x64 tiles with
-    a deep load ring at one block per CU or a short ring at several, 128x128
-    tiles once the grid gives every CU two), ragged M and N, bit-exact."""
+    """The group-64 MFMA GEMMs: the fragment-order kernel (K a multiple of
+    512) with one m-tile (32 x 128 tiles) or several (64 x 64 tiles), a
+    single w_s tile (K = 512) and an odd number of them (K = 1536), and the
+    row-major kernel for the other K; ragged M and N, bit-exact."""
     run_linear_case(orc, M, N, K, 64, seed=7 * M + N + K, groups=False)
 
 
-@pytest.mark.parametrize("M,N,K", [(100, 200, 1024), (333, 1030, 2048), (1030, 6200, 128)])
+@pytest.mark.parametrize("M,N,K", [(100, 200, 1024), (333, 1030, 2048), (70, 300, 1536), (1030, 6200, 1024),
+                                   (1030, 6200, 128)])
 def test_gemm_swiglu_ragged_parity(orc, M, N, K):
+    """SwiGLU GEMM: 64 x (64 + 64) tiles with 4-group w_s tiles (an odd
+    count at K = 1536), 128-row tiles once the grid outgrows one round of the
+    device (M = 1030), and the row-major kernel at K = 128."""
     A, Wg, Sg = make_case(900 + M, M, N, K, 64)
     _, Wu, Su = make_case(901 + M, M, N, K, 64)
     H = host(q.linear_i8_swiglu(dev(A), dev(Wg), dev(Sg), dev(Wu), dev(Su), 64))
