@@ -282,15 +282,20 @@ int run_linear(const float *A, int nseg, const int8_t *const *W, const float *co
             return Q3VL_OK;
         }
         for (int i = 0; i < nseg; ++i) {
-            float *Ci = C[i];
-            if (mode == GEMV_ARGMAX && !Ci) Ci = reinterpret_cast<float *>(wbase + LG.logits);
-            GemmMfArgs g{aq, asT, Mt, W[i], S[i], nullptr, nullptr, Ci, (int)M, (int)Ns[i], (int)K};
+            GemmMfArgs g{aq, asT, Mt, W[i], S[i], nullptr, nullptr, C[i], (int)M, (int)Ns[i], (int)K};
+            int nparts = 0;
+            if (mode == GEMV_ARGMAX) {
+                // the GEMM leaves each block's per-row argmax partial; the
+                // logits are stored only when the caller asked for them
+                g.part_val = reinterpret_cast<float *>(wbase + LG.parts_val);
+                g.part_idx = reinterpret_cast<int32_t *>(wbase + LG.parts_idx);
+                const int cols = gemm_mf_argmax_cols((int)M);
+                nparts = (int)((Ns[i] + cols - 1) / cols);
+                if ((size_t)nparts > kMaxGemvParts) return Q3VL_ERR_UNSUPPORTED;
+            }
             Q3VL_HIP(launch_gemm_mf(g, false, cus, st), "gemm launch");
             if (mode == GEMV_ARGMAX)
-                Q3VL_HIP(launch_argmax_rows(Ci, (int)M, (int)Ns[i],
-                                            reinterpret_cast<float *>(wbase + LG.parts_val),
-                                            reinterpret_cast<int32_t *>(wbase + LG.parts_idx),
-                                            kGemmArgmaxParts, ids, st),
+                Q3VL_HIP(launch_argmax_final(g.part_val, g.part_idx, nparts, (int)M, ids, st),
                          "argmax launch");
         }
         return Q3VL_OK;

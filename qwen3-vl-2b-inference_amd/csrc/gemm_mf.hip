@@ -458,7 +458,66 @@ __global__ __launch_bounds__(256, BPC) void gemm_mf_kernel(GemmMfArgs a) {
         for (int j = 0; j < SG; ++j) group(g0, j);
     }
 
-    // ---- store
+    // ---- greedy-argmax partials of the block's columns (plain products):
+    // per row the larger value, equal values the lower column, values that
+    // are not above -FLT_MAX (NaN, -inf, -FLT_MAX) never win -- the strict >
+    // scan from -FLT_MAX, as argmax_part_kernel combines it. Each lane
+    // reduces its TN columns, the 32 lanes of its half (one row per
+    // accumulator) by xor shuffles, the WN waves that share the rows through
+    // LDS (free: the last group's barrier has passed).
+    if constexpr (!SWIGLU) {
+        if (a.part_val) {  // uniform
+            float *rv = reinterpret_cast<float *>(smem);          // [4 waves][TM][16][2]
+            int32_t *ri = reinterpret_cast<int32_t *>(rv + 4 * TM * 32);
+#pragma unroll
+            for (int i = 0; i < TM; ++i) {
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    // rows 8 (e / 4) + (e % 4) and 4 more: past M for both
+                    // halves -> nothing to reduce (uniform)
+                    if (32 * (mt0 + wm * TM + i) + 8 * (e >> 2) + (e & 3) >= M) continue;
+                    float bv = -FLT_MAX;
+                    int32_t bi = -1;
+#pragma unroll
+                    for (int j = 0; j < TN; ++j) {
+                        const float v = out[i][j][e];
+                        if (ncol[j] < N && v > -FLT_MAX) am_combine(bv, bi, v, ncol[j]);
+                    }
+#pragma unroll
+                    for (int off = 16; off > 0; off >>= 1) {
+                        const float ov = __shfl_xor(bv, off);
+                        const int32_t oi = __shfl_xor(bi, off);
+                        am_combine(bv, bi, ov, oi);
+                    }
+                    if ((lane & 31) == 0) {
+                        rv[((wid * TM + i) * 16 + e) * 2 + h] = bv;
+                        ri[((wid * TM + i) * 16 + e) * 2 + h] = bi;
+                    }
+                }
+            }
+            lds_barrier();
+            if (tid < MTB * 32) {
+                const int li = tid >> 5, r = tid & 31;  // block m-tile li, row r of it
+                const int wmr = li / TM, i = li % TM;
+                const int e = 4 * (r >> 3) + (r & 3), hr = (r >> 2) & 1;
+                float bv = -FLT_MAX;
+                int32_t bi = -1;
+#pragma unroll
+                for (int w = 0; w < WN; ++w) {
+                    const int src = ((wmr + WM * w) * TM + i) * 16 + e;
+                    am_combine(bv, bi, rv[src * 2 + hr], ri[src * 2 + hr]);
+                }
+                const int mrow = 32 * (mt0 + li) + r;
+                if (mrow < M) {
+                    a.part_val[(size_t)(n0 / ncols) * M + mrow] = bv;
+                    a.part_idx[(size_t)(n0 / ncols) * M + mrow] = bi;
+                }
+            }
+        }
+    }
+
+    // ---- store (an argmax caller that wants no logits passes C = null)
+    if (!a.C) return;  // uniform
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
         const int rbase = 32 * (mt0 + wm * TM + i) + 4 * h;
@@ -506,8 +565,11 @@ bool gemm_mf_serves(int M, int N, int K, bool swiglu, int cus) {
     return K % (64 * kWsTile) == 0 && K > 0 && M >= 1 && N >= 1;  // whole w_s tiles
 }
 
+int gemm_mf_argmax_cols(int M) { return (M + 31) / 32 == 1 ? 128 : 64; }
+
 hipError_t launch_gemm_mf(const GemmMfArgs &a, bool swiglu, int cus, hipStream_t st) {
     if (a.K % (64 * kWsTile) != 0 || a.K <= 0 || a.M < 1 || a.N < 1) return hipErrorInvalidValue;
+    if (swiglu && a.part_val) return hipErrorInvalidValue;
     if (swiglu) {
         if (mf_blocks(a, 1, 64) <= 3L * cus) return launch_mf<1, 2, true, 2, 3, 2, true, 4>(a, st);
         return launch_mf<2, 2, true, 2, 2, 2, true, 8>(a, st);

@@ -43,15 +43,6 @@ __host__ __device__ __forceinline__ int group_ld(int Kg) {
     return ((k4 >> 2) & 1) ? k4 : k4 + 4;
 }
 
-// Combine rule equivalent to the sequential strict-> scan of greedy_decode:
-// the larger value wins, equal values keep the lower index, idx<0 is empty.
-__device__ __forceinline__ void am_combine(float &bv, int32_t &bi, float v, int32_t i) {
-    if (i < 0) return;
-    if (bi < 0 || v > bv || (v == bv && i < bi)) {
-        bv = v;
-        bi = i;
-    }
-}
 
 // Segment fields held in scalar registers. The kernel never indexes
 // a.seg[] with a run-time value: that would fetch the field from kernel
@@ -738,44 +729,43 @@ __device__ void am_block_reduce(float &bv, int32_t &bi) {
 
 // Reduces block partials [nparts, M] to ids[m] (empty partials have idx < 0;
 // none at all -> 0, as greedy_decode returns 0 when nothing beats -FLT_MAX).
-// 1024 threads, each issuing all of its (<= 8) loads before combining.
+// One 1024-thread block per row m, each thread issuing all of its (<= 8)
+// loads before combining.
 __global__ __launch_bounds__(1024) void argmax_final_kernel(const float *pv, const int32_t *pi,
                                                             int nparts, int M, int32_t *ids,
                                                             int32_t *pos_inc) {
     __shared__ float wv[16];
     __shared__ int32_t wi[16];
     const int tid = threadIdx.x;
-    for (int m = 0; m < M; ++m) {
-        float v[8];
-        int32_t ix[8];
+    const int m = blockIdx.x;
+    float v[8];
+    int32_t ix[8];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            const int p = tid + u * 1024;
-            v[u] = p < nparts ? pv[(size_t)p * M + m] : -FLT_MAX;
-            ix[u] = p < nparts ? pi[(size_t)p * M + m] : -1;
-        }
-        float bv = -FLT_MAX;
-        int32_t bi = -1;
-#pragma unroll
-        for (int u = 0; u < 8; ++u) am_combine(bv, bi, v[u], ix[u]);
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) {
-            const float ov = __shfl_xor(bv, off);
-            const int32_t oi = __shfl_xor(bi, off);
-            am_combine(bv, bi, ov, oi);
-        }
-        if ((tid & 63) == 0) {
-            wv[tid >> 6] = bv;
-            wi[tid >> 6] = bi;
-        }
-        __syncthreads();
-        if (tid == 0) {
-            for (int w = 1; w < 16; ++w) am_combine(bv, bi, wv[w], wi[w]);
-            ids[m] = bi < 0 ? 0 : bi;
-        }
-        __syncthreads();
+    for (int u = 0; u < 8; ++u) {
+        const int p = tid + u * 1024;
+        v[u] = p < nparts ? pv[(size_t)p * M + m] : -FLT_MAX;
+        ix[u] = p < nparts ? pi[(size_t)p * M + m] : -1;
     }
-    if (tid == 0 && pos_inc) *pos_inc += 1;
+    float bv = -FLT_MAX;
+    int32_t bi = -1;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) am_combine(bv, bi, v[u], ix[u]);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(bv, off);
+        const int32_t oi = __shfl_xor(bi, off);
+        am_combine(bv, bi, ov, oi);
+    }
+    if ((tid & 63) == 0) {
+        wv[tid >> 6] = bv;
+        wi[tid >> 6] = bi;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        for (int w = 1; w < 16; ++w) am_combine(bv, bi, wv[w], wi[w]);
+        ids[m] = bi < 0 ? 0 : bi;
+        if (pos_inc && m == 0) *pos_inc += 1;
+    }
 }
 
 // Stand-alone argmax over logits rows: block b scans a contiguous slice with
@@ -936,7 +926,8 @@ hipError_t launch_gemv(const GemvArgs &a, bool lanes, int *grid_out, hipStream_t
 hipError_t launch_argmax_final(const float *pv, const int32_t *pi, int nparts, int M,
                                int32_t *ids, hipStream_t st, int32_t *pos_inc) {
     if (nparts > 8192) return hipErrorInvalidValue;
-    argmax_final_kernel<<<1, 1024, 0, st>>>(pv, pi, nparts, M, ids, pos_inc);
+    if (M < 1) return hipErrorInvalidValue;
+    argmax_final_kernel<<<M, 1024, 0, st>>>(pv, pi, nparts, M, ids, pos_inc);
     return hipGetLastError();
 }
 

@@ -8,6 +8,7 @@
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <cfloat>
 
 #ifndef Q3VL_INLINE
 #define Q3VL_INLINE __device__ __forceinline__
@@ -117,6 +118,16 @@ Q3VL_INLINE float silu_mul(float gv, float uv) {
     const float den = 1.0f + expf_host(-gv);
     const float sl = (float)((double)gv / (double)den);
     return sl * uv;
+}
+
+// Combine rule equivalent to the sequential strict-> scan of greedy_decode:
+// the larger value wins, equal values keep the lower index, idx<0 is empty.
+__device__ __forceinline__ void am_combine(float &bv, int32_t &bi, float v, int32_t i) {
+    if (i < 0) return;
+    if (bi < 0 || v > bv || (v == bv && i < bi)) {
+        bv = v;
+        bi = i;
+    }
 }
 
 // Workgroup barrier that orders LDS only: global loads stay in flight across

@@ -128,7 +128,14 @@ struct GemmMfArgs {
     const float *S1;
     float *C;            // [M, N] (H when swiglu)
     int M, N, K;
+    // optional (not with swiglu): greedy-argmax partials of each block's
+    // columns per row, [ceil(N / gemm_mf_argmax_cols(...))][M], for
+    // launch_argmax_final
+    float *part_val = nullptr;
+    int32_t *part_idx = nullptr;
 };
+// Columns per argmax partial of launch_gemm_mf for an M-row plain product.
+int gemm_mf_argmax_cols(int M);
 // qf must hold 32*ceil(M/32)*K halves, asf 32*ceil(M/32)*K/64 floats.
 hipError_t launch_quantize_frag(const float *A, _Float16 *qf, float *asf, int M, int K,
                                 hipStream_t st);

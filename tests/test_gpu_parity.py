@@ -288,6 +288,31 @@ def test_lm_head_argmax_gemm_path(orc, M, V, K):
     np.testing.assert_array_equal(ids, ids_ref)
 
 
+def test_lm_head_argmax_gemm_special_values(orc):
+    """Argmax partials fused into the GEMM: a row of NaN logits (id 0), a
+    column made +-inf/NaN by an infinite weight scale, a column whose logits
+    are all -inf; ids equal the greedy scan of the oracle's logits, with and
+    without the logits stored."""
+    M, V, K, gs = 12, 5000, 1024, 64
+    A, W, S = make_case(4242, M, V, K, gs)
+    A[5, :] = np.nan
+    S[17, 3] = np.inf
+    W[33, :] = -127
+    S[33, :] = np.float32(3e38)
+    A[7, :] = np.abs(A[7, :]) + 0.5  # row 7: column 33 -> -inf
+    logits_ref = orc.linear(A, W, S, gs)
+    ids_ref = orc.argmax_rows(logits_ref)
+    assert ids_ref[5] == 0 and np.isneginf(logits_ref[7, 33])
+    logits = torch.empty((M, V), dtype=torch.float32, device="cuda")
+    ids = host(q.lm_head_argmax(dev(A), dev(W), dev(S), gs, logits=logits))
+    np.testing.assert_array_equal(ids, ids_ref)
+    got = host(logits)
+    nan = np.isnan(logits_ref)
+    assert np.array_equal(np.isnan(got), nan)
+    np.testing.assert_array_equal(got[~nan].view(np.uint32), logits_ref[~nan].view(np.uint32))
+    np.testing.assert_array_equal(host(q.lm_head_argmax(dev(A), dev(W), dev(S), gs)), ids_ref)
+
+
 def test_argmax_rows_special_values(orc):
     fmax = np.finfo(np.float32).max
     rows = np.full((6, 3000), -np.inf, np.float32)
