@@ -629,8 +629,8 @@ def bench_cfg2(args):
     tops = ops / (ms * 1e-3) / 1e12
     return dict(name="cfg2_prefill_gemm", metric="TOPS", value=tops, ms=ms, algo_ops=ops,
                 frac=tops / FP16_PEAK_TFLOPS, frac_of_int8_peak=tops / INT8_PEAK_TOPS,
-                kernel="gate|up: quantize_frag_kernel + gemm_mf_kernel (SwiGLU epilogue); "
-                       "down: quantize_rows_kernel + gemm_g64_kernel")
+                kernel="quantize_frag_kernel + gemm_mf_kernel: gate|up with the SwiGLU "
+                       "epilogue, then down")
 
 
 def bench_cfg3(args, M):
@@ -684,8 +684,8 @@ def bench_cfg4(args):
     return dict(name="cfg4_vision_linears", metric="TOPS", value=tops, ms=ms, algo_ops=ops,
                 frac=tops / FP16_PEAK_TFLOPS, frac_of_int8_peak=tops / INT8_PEAK_TOPS,
                 gemms=B * len(VIS_SHAPES) + len(MERGER_SHAPES),
-                kernel="by shape: quantize_frag_kernel + gemm_mf_kernel, or "
-                       "quantize_rows_kernel + gemm_g64_kernel")
+                kernel="quantize_frag_kernel + gemm_mf_kernel (K a multiple of 512: every "
+                       "vision and merger linear)")
 
 
 # ------------------------------------------------- checkpoint files

@@ -540,6 +540,8 @@ template <int TM, int TN, bool SWIGLU, int D, int BPC, int WM = 2, bool AL = tru
 static hipError_t launch_mf(const GemmMfArgs &a, hipStream_t st) {
     constexpr int BN = 32 * (4 / WM) * TN, MTB = WM * TM;
     const int ncols = SWIGLU ? BN / 2 : BN;
+    // argmax partials: one per block column range, counted by the caller
+    if (a.part_val && ncols != gemm_mf_argmax_cols(a.M)) return hipErrorInvalidValue;
     const int tiles = ((a.N + ncols - 1) / ncols) * ((a.Mt + MTB - 1) / MTB);
     const int grid = 8 * ((tiles + 7) / 8);  // see the tile order in the kernel
     const size_t lds = 2 * (BN / 32) * 4 * 64 * 16 + (AL ? 2 * MTB * 4096 : 0) + 2 * 32 * MTB * 4 + 2 * SG * BN * 4;
@@ -567,6 +569,8 @@ bool gemm_mf_serves(int M, int N, int K, bool swiglu, int cus) {
     return K % (64 * kWsTile) == 0 && K > 0 && M >= 1 && N >= 1;  // whole w_s tiles
 }
 
+// The output columns per block of the plain tiles launch_gemm_mf picks
+// below (32 x 128 for one m-tile, 64 x 64 otherwise): one argmax partial each.
 int gemm_mf_argmax_cols(int M) { return (M + 31) / 32 == 1 ? 128 : 64; }
 
 hipError_t launch_gemm_mf(const GemmMfArgs &a, bool swiglu, int cus, hipStream_t st) {
