@@ -22,10 +22,13 @@
 // per weight row at a time, come in tiles of several groups:
 // * A: the quantizer writes q in fragment order -- per 32-row m-tile t and
 //   group g a 4 KB chunk [slice s][lane l][8 halves] holding
-//   q[32t + l%32][64g + 32(l/32) + 8s + j]. Wave w loads slice w of each of
-//   the block's m-tiles (one coalesced 1 KB read each) and stores it to LDS
-//   unchanged; every wave then reads its fragments with one ds_read_b128 per
-//   slice and m-tile. The a_s come in the matching order: [t][g][l/32][16]
+//   q[32t + l%32][64g + 32(l/32) + 8s + j]. Either (AL) wave w loads slice w
+//   of each of the block's m-tiles (one coalesced 1 KB read each) and stores
+//   it to LDS unchanged, every wave then reading its fragments with one
+//   ds_read_b128 per slice and m-tile; or each wave loads the four slices
+//   of its own m-tiles straight into its registers (the L1 path carries A,
+//   LDS only B and the scales: faster wherever two or more m-tiles share a
+//   block). The a_s come in the matching order: [t][g][l/32][16]
 //   holds a_s of rows 32t + 8(e/4) + 4(l/32) + e%4, the rows a lane's 16
 //   accumulators hold.
 // * B: the block loads its weight rows (64 bytes per row and group) once,
@@ -34,9 +37,9 @@
 //   fragments with one ds_read_b128 per slice and n-tile. The 16-byte slots
 //   are swizzled (slot ^ 4*(s/2) ^ 8*(l/32)) so that the writers' and the
 //   readers' 16-lane passes each hit 16 distinct bank groups.
-// * w_s: every SG groups (8, or 4 where three blocks' LDS must fit) the
-//   block loads the next SG scales of each of its weight rows, 2 threads per
-//   row, contiguous 4 SG bytes per row, into a second LDS tile slot.
+// * w_s: every SG groups (8) the block loads the next SG scales of each of
+//   its weight rows, 2 threads per row, contiguous 4 SG bytes per row, into
+//   a second LDS tile slot.
 // * The k order inside a group: slice s of lane half h covers k = 32h + 8s +
 //   j; A and B use the same map, so each MFMA pairs matching k and the four
 //   slices cover the group's 64 k once.
@@ -553,8 +556,8 @@ static hipError_t launch_mf(const GemmMfArgs &a, hipStream_t st) {
 // and with which tiles, from timings of the prefill, vision and lm_head
 // shapes on MI355X: every group-64 product whose K is a whole number of w_s
 // tiles (K % 512 == 0). SwiGLU: 64 x (64 gate + 64 up) tiles at 3 blocks per
-// CU (4-group w_s tiles, so three blocks' LDS fit) while the grid fits one
-// round of the device, else 128-row tiles at 2 blocks per CU. Plain: one
+// CU, each wave loading its own A slices, while the grid fits one round of
+// the device, else 128-row tiles at 2 blocks per CU. Plain: one
 // m-tile (M <= 32, e.g. the lm_head over a few rows) takes 32 x 128 tiles of
 // 1 x 4 waves, its A staged once per block; more m-tiles take 64 x 64 tiles
 // at 4 blocks per CU, each wave loading its A slices itself (3-8% faster
@@ -577,7 +580,7 @@ hipError_t launch_gemm_mf(const GemmMfArgs &a, bool swiglu, int cus, hipStream_t
     if (a.K % (64 * kWsTile) != 0 || a.K <= 0 || a.M < 1 || a.N < 1) return hipErrorInvalidValue;
     if (swiglu && a.part_val) return hipErrorInvalidValue;
     if (swiglu) {
-        if (mf_blocks(a, 1, 64) <= 3L * cus) return launch_mf<1, 2, true, 2, 3, 2, true, 4>(a, st);
+        if (mf_blocks(a, 1, 64) <= 3L * cus) return launch_mf<1, 2, true, 2, 3, 2, false, 8>(a, st);
         return launch_mf<2, 2, true, 2, 2, 2, true, 8>(a, st);
     }
     if (a.Mt == 1) return launch_mf<1, 1, false, 2, 3, 1, true, 8>(a, st);
