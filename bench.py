@@ -579,7 +579,7 @@ def decode_gemv_roofline(model, dims):
     step_bytes = sum(res[k]["bytes"] * n for k, n in per_step.items())
     launches = sum(per_step.values())
     gbs = step_bytes / (step_us * 1e-6) / 1e9
-    return dict(kernel="gemv_kernel<64, 1, true, R, KC, MD> (the decode step's GEMV launches)",
+    return dict(kernel="gemv_kernel<64, 1, true, R, KC, MD, P> (the decode step's GEMV launches)",
                 launches=launches,
                 bytes_per_launch=step_bytes / launches, avg_launch_us=step_us / launches,
                 achieved_GBs=gbs, frac=gbs / HBM_PEAK_GBS, step_gemv_us=step_us, by_class=res)
@@ -605,7 +605,7 @@ def bench_cfg0(args):
     return dict(name="cfg0_up_proj_gemv", metric="GB/s", value=gbs, ms=ms, eager_ms=eager_ms,
                 algo_bytes=algo, frac=gbs / HBM_PEAK_GBS, copies=n,
                 timing="HIP-graph replay of one launch per weight copy (eager_ms: per Python call)",
-                kernel="gemv_kernel<64, 1, true, 4, 2048, 0>")
+                kernel="gemv_kernel<64, 1, true, 2, 2048, 0, 4>")
 
 
 def bench_cfg2(args):

@@ -34,6 +34,7 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr int GEMV_R = 8;          // weight rows per tile (general path; the lane path picks 2, 4 or 8)
 constexpr int GEMV_MAX_THREADS = 512;  // => K <= 8192 on this path
 constexpr int GEMV_MAX_GRID = 8192;    // the C ABI reserves this many argmax partials
+constexpr int kSubGroups = 4;          // row tiles per block at K = 2048, group 64
 
 // Row stride (in words) of the per-row group buffers: a multiple of 4 whose
 // quarter is odd, so 16 lanes reading 16 bytes each at consecutive rows hit
@@ -98,8 +99,16 @@ __host__ __device__ constexpr int norm_row_words(int K, bool seg) {
 // MD: the launch's mode and segment count when fixed at compile time
 // (GemvMd), so that segment selection folds away; MD_RUNTIME reads them
 // from the arguments.
-template <int GS, int MR, bool LANES, int R, int KC, int MD>
+// P: row tiles a block works on side by side. With P > 1 the block is P
+// sub-groups of K/16 threads, sub-group p taking tiles blockIdx.x*P + p (grid
+// stride gridDim.x*P); the activation row is staged, normalized and quantized
+// once for all of them, with the staging spread over the whole block, so a CU
+// no longer repeats that work for every resident block. (Decode shapes:
+// K = 2048, group 64, one activation row.)
+template <int GS, int MR, bool LANES, int R, int KC, int MD, int P = 1>
 __global__ __launch_bounds__(GEMV_MAX_THREADS) void gemv_kernel(GemvArgs a, int ntiles) {
+    static_assert(P == 1 || (P == 4 && KC == 2048 && GS == 64 && MR == 1 && LANES),
+                  "shared-prologue blocks serve the decode shapes only");
     constexpr int T = GS / 16;
     constexpr int HALF = R / 2;
     // scale values per thread per tile: R*Kg <= (16R/GS) * nthr since nthr >= K/16
@@ -110,7 +119,9 @@ __global__ __launch_bounds__(GEMV_MAX_THREADS) void gemv_kernel(GemvArgs a, int 
     const int K = KC ? KC : a.K;
     const int Kg = K / GS;
     const int M = a.M;
-    const int tid = threadIdx.x;
+    // thread index within the sub-group (the K-chunk it owns) and sub-group
+    const int tid = P > 1 ? (int)(threadIdx.x & 127) : (int)threadIdx.x;
+    const int sub = P > 1 ? (int)(threadIdx.x >> 7) : 0;
     const int nthr = KC ? (KC / 16 > 64 ? KC / 16 : 64) : (int)blockDim.x;  // max(K/16, 64)
     const int nchunk = K / 16;
     const bool act = tid < nchunk;   // owns a 16-byte K-chunk
@@ -175,15 +186,19 @@ __global__ __launch_bounds__(GEMV_MAX_THREADS) void gemv_kernel(GemvArgs a, int 
     // threads of a wave, each reading its own group, hit distinct banks.
     const int xpad = 4 * (16 * nthr / GS);
     const int stage_need = 16 * nthr + xpad + (has_norm ? 8 * nrs : 0);
-    int stage_words = acc_words > stage_need ? acc_words : stage_need;
-    int32_t *accb = reinterpret_cast<int32_t *>(smem);
+    // (one accb per sub-group; all of them alias the phase-0 staging)
+    const int stage_words = P * acc_words > stage_need ? P * acc_words : stage_need;
+    int32_t *accb = reinterpret_cast<int32_t *>(smem) + sub * acc_words;
     float *xs = reinterpret_cast<float *>(smem);  // phase 0 only (aliases accb)
     float *xn = xs + 16 * nthr + xpad;            // [8][nrs]: x[l + 8j] at l*nrs + j
     // element e of the staged row (groups padded by 4 floats)
     auto xpos = [&](int e) { return e + 4 * (e / GS); };
     float *as_l = reinterpret_cast<float *>(smem) + stage_words;  // [M][Kg]
-    float *sc_l = as_l + MR * Kg;                                   // [R][ld]
-    float *ybuf = sc_l + R * ld;                                    // [MR][R]
+    // P > 1: the quantized row, 8 words (16 int16) per K-chunk, handed from
+    // the threads that quantize it to every sub-group
+    uint32_t *qs = reinterpret_cast<uint32_t *>(as_l + MR * Kg);
+    float *sc_l = reinterpret_cast<float *>(qs + (P > 1 ? 8 * nthr : 0)) + sub * R * ld;  // [P][R][ld]
+    float *ybuf = reinterpret_cast<float *>(qs + (P > 1 ? 8 * nthr : 0)) + P * R * ld + sub * MR * R;  // [P][MR][R]
 
     // Weight chunk and scale prefetch for one tile (registers).
     u32x4 wv[R];
@@ -210,259 +225,337 @@ __global__ __launch_bounds__(GEMV_MAX_THREADS) void gemv_kernel(GemvArgs a, int 
         }
     };
 
-    int tile = blockIdx.x;
+    // this sub-group's first tile; a block's sub-groups advance together (a
+    // sub-group past the last tile runs it with no valid rows), so every
+    // barrier below is reached by the whole block
+    int tile = blockIdx.x * P + sub;
 
     // ---- phase 0: quantize the activation rows (reference i8:135-177).
     // Row 0's loads are issued before the first tile's weight loads so that
     // waiting for them does not wait for the weights.
-    uint32_t qp[MR][8];
-#pragma unroll
-    for (int m = 0; m < MR; ++m) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) qp[m][j] = 0;
-        if (m >= M) continue;  // uniform: every thread skips together
-        const float4 *src = reinterpret_cast<const float4 *>(Ap + (size_t)m * K);
-        // four float4 per thread cover K/4 <= 4 * nthr (named registers; an
-        // array here ends up in scratch memory)
-        const int i0 = tid, i1 = tid + nthr, i2 = tid + 2 * nthr, i3 = tid + 3 * nthr;
-        const float4 x0 = src[i0 < K / 4 ? i0 : 0];
-        const float4 x1 = src[i1 < K / 4 ? i1 : 0];
-        const float4 x2 = src[i2 < K / 4 ? i2 : 0];
-        const float4 x3 = src[i3 < K / 4 ? i3 : 0];
-        // fused norm: this thread's 16 weight bytes and group scale
-        // (loaded unconditionally, from the activation row when there is no
-        // norm, so that no later wait depends on which loads were issued)
-        const int8_t *nwp = has_norm ? norm_w : reinterpret_cast<const int8_t *>(Ap);
-        const float *nsp = has_norm ? norm_s : Ap;
-        const u32x4 nw = *reinterpret_cast<const u32x4 *>(nwp + 16 * (act ? tid : 0));
-        const float nsc = nsp[act ? (16 * tid) / GS : 0];
-        if (m == 0) prefetch(resolve(tile));  // grid <= ntiles: every block has a tile
-        // keep the loads above ahead of the LDS stores below (the stores wait
-        // only for the activation loads, issued first); slots past K/4 exist
-        // (stage_words >= 16 * nthr + padding) and are never read
-        __builtin_amdgcn_sched_barrier(0);
-        float4 *xs4 = reinterpret_cast<float4 *>(xs);
-        xs4[xpos(4 * i0) / 4] = x0;
-        xs4[xpos(4 * i1) / 4] = x1;
-        xs4[xpos(4 * i2) / 4] = x2;
-        xs4[xpos(4 * i3) / 4] = x3;
-        if (has_norm) {
-            // chain-major copy: element 4i + c sits in chain 4*(i&1) + c at i/2
-            auto put4 = [&](int i, const float4 &v) {
-                if (i < K / 4) {
-                    const int t = i >> 1;  // position in the chain
-                    float *d = xn + 4 * (i & 1) * nrs + (SEGN ? t + 4 * (t >> 5) : t);
-                    d[0] = v.x;
-                    d[nrs] = v.y;
-                    d[2 * nrs] = v.z;
-                    d[3 * nrs] = v.w;
-                }
-            };
-            put4(i0, x0);
-            put4(i1, x1);
-            put4(i2, x2);
-            put4(i3, x3);
+    //
+    // The fused norm's chain-major copy of float4 i of the staged row:
+    // element 4i + c sits in chain 4*(i&1) + c at i/2.
+    auto put4 = [&](int i, const float4 &v) {
+        if (i < K / 4) {
+            const int t = i >> 1;  // position in the chain
+            float *d = xn + 4 * (i & 1) * nrs + (SEGN ? t + 4 * (t >> 5) : t);
+            d[0] = v.x;
+            d[nrs] = v.y;
+            d[2 * nrs] = v.z;
+            d[3 * nrs] = v.w;
         }
-        lds_barrier();
-        if (has_norm) {
-            // sum of squares in the reference's 8-lane order (lanes 0..7 of
-            // wave 0), then inv = 1/sqrt(ss/K + eps) in fp32
-            if (SEGN && tid < 64) {
-                // lane 8l + j holds segment j (positions 32j .. 32j+31) of
-                // chain l in registers. Segment s: every lane runs its 32
-                // FMAs, but only lanes j == s carry their chain (the others'
-                // sums are discarded); a row shift then hands each chain's
-                // sum to the lane of its next segment. So chain l is the
-                // reference's FMA sequence over t = 0..255, with no LDS read
-                // between its FMAs.
-                const float *sg = xn + (tid >> 3) * nrs + (tid & 7) * 36;
-                float4 X[8];
+    };
+    // The fused norm: sum of squares in the reference's 8-lane order (lanes
+    // 0..7 of the block's wave 0), then inv = 1/sqrt(ss/K + eps) in fp32.
+    auto norm_chain = [&]() {
+        if (SEGN && threadIdx.x < 64) {
+            // lane 8l + j holds segment j (positions 32j .. 32j+31) of
+            // chain l in registers. Segment s: every lane runs its 32
+            // FMAs, but only lanes j == s carry their chain (the others'
+            // sums are discarded); a row shift then hands each chain's
+            // sum to the lane of its next segment. So chain l is the
+            // reference's FMA sequence over t = 0..255, with no LDS read
+            // between its FMAs.
+            const float *sg = xn + (tid >> 3) * nrs + (tid & 7) * 36;
+            float4 X[8];
 #pragma unroll
-                for (int u = 0; u < 8; ++u) X[u] = reinterpret_cast<const float4 *>(sg)[u];
-                float acc = 0.0f;
+            for (int u = 0; u < 8; ++u) X[u] = reinterpret_cast<const float4 *>(sg)[u];
+            float acc = 0.0f;
 #pragma unroll
-                for (int sgm = 0; sgm < 8; ++sgm) {
+            for (int sgm = 0; sgm < 8; ++sgm) {
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    acc = fmaf(X[u].x, X[u].x, acc);
+                    acc = fmaf(X[u].y, X[u].y, acc);
+                    acc = fmaf(X[u].z, X[u].z, acc);
+                    acc = fmaf(X[u].w, X[u].w, acc);
+                }
+                if (sgm < 7)  // row_shr:1 (lane i takes lane i-1 inside each row of 16)
+                    acc = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                              0, __builtin_bit_cast(int, acc), 0x111, 0xF, 0xF, false));
+            }
+            // chain l's sum sits in lane 8l + 7; added in chain order
+            float ss = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, acc), 7));
+#pragma unroll
+            for (int l = 1; l < 8; ++l)
+                ss = ss + __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, acc), 8 * l + 7));
+            if (threadIdx.x == 0) s_norm_inv = rcp_rn(sqrt_rn(ss * rcp_rn((float)K) + a.norm_eps));
+        } else if (threadIdx.x < 64) {
+            float acc = 0.0f;
+            if (tid < 8) {
+                const float *row = xn + tid * nrs;
+                const int cnt = K / 8;
+                // batches of 32 in two register sets used in turn: the
+                // next batch's reads are in flight during this batch's
+                // FMAs (s_waitcnt lgkmcnt(0) before issuing them: two
+                // batches of 8 reads exceed what the 4-bit counter tells
+                // apart)
+                float4 A[8], B[8];
+                auto ld = [&](float4 *D, int i) {
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) D[u] = reinterpret_cast<const float4 *>(row + i)[u];
+                };
+                auto sq = [&](const float4 *D) {
 #pragma unroll
                     for (int u = 0; u < 8; ++u) {
-                        acc = fmaf(X[u].x, X[u].x, acc);
-                        acc = fmaf(X[u].y, X[u].y, acc);
-                        acc = fmaf(X[u].z, X[u].z, acc);
-                        acc = fmaf(X[u].w, X[u].w, acc);
+                        acc = fmaf(D[u].x, D[u].x, acc);
+                        acc = fmaf(D[u].y, D[u].y, acc);
+                        acc = fmaf(D[u].z, D[u].z, acc);
+                        acc = fmaf(D[u].w, D[u].w, acc);
                     }
-                    if (sgm < 7)  // row_shr:1 (lane i takes lane i-1 inside each row of 16)
-                        acc = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
-                                  0, __builtin_bit_cast(int, acc), 0x111, 0xF, 0xF, false));
-                }
-                // chain l's sum sits in lane 8l + 7; added in chain order
-                float ss = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, acc), 7));
-#pragma unroll
-                for (int l = 1; l < 8; ++l)
-                    ss = ss + __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, acc), 8 * l + 7));
-                if (tid == 0) s_norm_inv = rcp_rn(sqrt_rn(ss * rcp_rn((float)K) + a.norm_eps));
-            } else if (tid < 64) {
-                float acc = 0.0f;
-                if (tid < 8) {
-                    const float *row = xn + tid * nrs;
-                    const int cnt = K / 8;
-                    // batches of 32 in two register sets used in turn: the
-                    // next batch's reads are in flight during this batch's
-                    // FMAs (s_waitcnt lgkmcnt(0) before issuing them: two
-                    // batches of 8 reads exceed what the 4-bit counter tells
-                    // apart)
-                    float4 A[8], B[8];
-                    auto ld = [&](float4 *D, int i) {
-#pragma unroll
-                        for (int u = 0; u < 8; ++u) D[u] = reinterpret_cast<const float4 *>(row + i)[u];
-                    };
-                    auto sq = [&](const float4 *D) {
-#pragma unroll
-                        for (int u = 0; u < 8; ++u) {
-                            acc = fmaf(D[u].x, D[u].x, acc);
-                            acc = fmaf(D[u].y, D[u].y, acc);
-                            acc = fmaf(D[u].z, D[u].z, acc);
-                            acc = fmaf(D[u].w, D[u].w, acc);
-                        }
-                    };
-                    int j = 0;
-                    if (cnt >= 32) {
-                        ld(A, 0);
-                        for (; j + 64 <= cnt; j += 64) {
-                            __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
-                            __builtin_amdgcn_sched_barrier(0);
-                            ld(B, j + 32);
-                            sq(A);
-                            __builtin_amdgcn_sched_barrier(0);
-                            __builtin_amdgcn_s_waitcnt(0xC07F);
-                            __builtin_amdgcn_sched_barrier(0);
-                            ld(A, j + 64 + 32 <= cnt ? j + 64 : j);  // (re-read when no batch is left)
-                            sq(B);
-                            __builtin_amdgcn_sched_barrier(0);
-                        }
-                        if (j + 32 <= cnt) {  // A holds j .. j+31
-                            __builtin_amdgcn_s_waitcnt(0xC07F);
-                            sq(A);
-                            j += 32;
-                        }
+                };
+                int j = 0;
+                if (cnt >= 32) {
+                    ld(A, 0);
+                    for (; j + 64 <= cnt; j += 64) {
+                        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+                        __builtin_amdgcn_sched_barrier(0);
+                        ld(B, j + 32);
+                        sq(A);
+                        __builtin_amdgcn_sched_barrier(0);
+                        __builtin_amdgcn_s_waitcnt(0xC07F);
+                        __builtin_amdgcn_sched_barrier(0);
+                        ld(A, j + 64 + 32 <= cnt ? j + 64 : j);  // (re-read when no batch is left)
+                        sq(B);
+                        __builtin_amdgcn_sched_barrier(0);
                     }
-                    for (; j < cnt; ++j) acc = fmaf(row[j], row[j], acc);
+                    if (j + 32 <= cnt) {  // A holds j .. j+31
+                        __builtin_amdgcn_s_waitcnt(0xC07F);
+                        sq(A);
+                        j += 32;
+                    }
                 }
-                float ss = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, acc), 0));
-#pragma unroll
-                for (int l = 1; l < 8; ++l)
-                    ss = ss + __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, acc), l));
-                if (tid == 0) s_norm_inv = rcp_rn(sqrt_rn(ss * rcp_rn((float)K) + a.norm_eps));
+                for (; j < cnt; ++j) acc = fmaf(row[j], row[j], acc);
             }
-            lds_barrier();
-            if (act) {
-                // this thread's 16 elements: x = w * ((s_g * inv) * x)
-                const float comb = nsc * s_norm_inv;
-                const uint32_t wd[4] = {nw.x, nw.y, nw.z, nw.w};
-                float4 *xc4 = reinterpret_cast<float4 *>(xs + xpos(16 * tid));
+            float ss = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, acc), 0));
 #pragma unroll
-                for (int q4 = 0; q4 < 4; ++q4) {
-                    float4 v = xc4[q4];
-                    const uint32_t w = wd[q4];
-                    v.x = (float)(int8_t)(w & 0xFF) * (comb * v.x);
-                    v.y = (float)(int8_t)((w >> 8) & 0xFF) * (comb * v.y);
-                    v.z = (float)(int8_t)((w >> 16) & 0xFF) * (comb * v.z);
-                    v.w = (float)(int8_t)(w >> 24) * (comb * v.w);
-                    xc4[q4] = v;
-                }
-            }
-            lds_barrier();
+            for (int l = 1; l < 8; ++l)
+                ss = ss + __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, acc), l));
+            if (threadIdx.x == 0) s_norm_inv = rcp_rn(sqrt_rn(ss * rcp_rn((float)K) + a.norm_eps));
         }
-        if (act) {
-            // The group's sum of squares in the reference order: 16 FMA
-            // chains (chain c takes elements 16t + c over the gs/16 steps t),
-            // V[i] = P[i] + P[i+8], then the fixed tree.
-            float sumsq;
-            if constexpr (T == 4) {
-                // The group's 4 threads are one lane quad; thread tg runs
-                // chains 4tg .. 4tg+3 (one 16-byte read per step). Lanes 0/1
-                // take the P[i+8] of lanes 2/3, and lane 0 takes lane 1's
-                // half of V (DPP quad permutes): the same adds in the same
-                // order, with 4 LDS reads instead of the whole group.
-                const float *xg = xs + g * (GS + 4);
-                float4 cv[4];
+    };
+    uint32_t qp[MR][8];
+    // The quantizer of K-chunk tid of activation row m.
+    auto quant_chunk = [&](int m) {
+        // The group's sum of squares in the reference order: 16 FMA
+        // chains (chain c takes elements 16t + c over the gs/16 steps t),
+        // V[i] = P[i] + P[i+8], then the fixed tree.
+        float sumsq;
+        if constexpr (T == 4) {
+            // The group's 4 threads are one lane quad; thread tg runs
+            // chains 4tg .. 4tg+3 (one 16-byte read per step). Lanes 0/1
+            // take the P[i+8] of lanes 2/3, and lane 0 takes lane 1's
+            // half of V (DPP quad permutes): the same adds in the same
+            // order, with 4 LDS reads instead of the whole group.
+            const float *xg = xs + g * (GS + 4);
+            float4 cv[4];
 #pragma unroll
-                for (int t = 0; t < 4; ++t) cv[t] = *reinterpret_cast<const float4 *>(xg + 16 * t + 4 * tg);
-                float p0 = 0.0f, p1 = 0.0f, p2 = 0.0f, p3 = 0.0f;
+            for (int t = 0; t < 4; ++t) cv[t] = *reinterpret_cast<const float4 *>(xg + 16 * t + 4 * tg);
+            float p0 = 0.0f, p1 = 0.0f, p2 = 0.0f, p3 = 0.0f;
 #pragma unroll
-                for (int t = 0; t < 4; ++t) {
-                    p0 = fmaf(cv[t].x, cv[t].x, p0);
-                    p1 = fmaf(cv[t].y, cv[t].y, p1);
-                    p2 = fmaf(cv[t].z, cv[t].z, p2);
-                    p3 = fmaf(cv[t].w, cv[t].w, p3);
-                }
+            for (int t = 0; t < 4; ++t) {
+                p0 = fmaf(cv[t].x, cv[t].x, p0);
+                p1 = fmaf(cv[t].y, cv[t].y, p1);
+                p2 = fmaf(cv[t].z, cv[t].z, p2);
+                p3 = fmaf(cv[t].w, cv[t].w, p3);
+            }
 #define Q3VL_QUAD(v, ctrl) \
-    __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), ctrl, 0xF, 0xF, false))
-                // quad_perm [2,3,2,3]: lanes 0, 1 read lanes 2, 3
-                const float v0 = p0 + Q3VL_QUAD(p0, 0xEE), v1 = p1 + Q3VL_QUAD(p1, 0xEE);
-                const float v2 = p2 + Q3VL_QUAD(p2, 0xEE), v3 = p3 + Q3VL_QUAD(p3, 0xEE);
-                // quad_perm [1,1,1,1]: lane 1's V[4..7]
-                const float w0 = Q3VL_QUAD(v0, 0x55), w1 = Q3VL_QUAD(v1, 0x55);
-                const float w2 = Q3VL_QUAD(v2, 0x55), w3 = Q3VL_QUAD(v3, 0x55);
-                // lane 0's value to the quad (quad_perm [0,0,0,0])
-                sumsq = Q3VL_QUAD(tree8(v0, v1, v2, v3, w0, w1, w2, w3), 0x00);
+__builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), ctrl, 0xF, 0xF, false))
+            // quad_perm [2,3,2,3]: lanes 0, 1 read lanes 2, 3
+            const float v0 = p0 + Q3VL_QUAD(p0, 0xEE), v1 = p1 + Q3VL_QUAD(p1, 0xEE);
+            const float v2 = p2 + Q3VL_QUAD(p2, 0xEE), v3 = p3 + Q3VL_QUAD(p3, 0xEE);
+            // quad_perm [1,1,1,1]: lane 1's V[4..7]
+            const float w0 = Q3VL_QUAD(v0, 0x55), w1 = Q3VL_QUAD(v1, 0x55);
+            const float w2 = Q3VL_QUAD(v2, 0x55), w3 = Q3VL_QUAD(v3, 0x55);
+            // lane 0's value to the quad (quad_perm [0,0,0,0])
+            sumsq = Q3VL_QUAD(tree8(v0, v1, v2, v3, w0, w1, w2, w3), 0x00);
 #undef Q3VL_QUAD
-            } else {
-                // every thread of the group runs all 16 chains from LDS (all
-                // of the group's reads are issued before the first FMA: one
-                // read latency instead of one per pair of reads)
-                float P[16];
+        } else {
+            // every thread of the group runs all 16 chains from LDS (all
+            // of the group's reads are issued before the first FMA: one
+            // read latency instead of one per pair of reads)
+            float Pc[16];
 #pragma unroll
-                for (int i = 0; i < 16; ++i) P[i] = 0.0f;
-                const float *xg = xs + g * (GS + 4);
-                constexpr int TB = T < 4 ? T : 4;  // sub-blocks of 16 read per batch
+            for (int i = 0; i < 16; ++i) Pc[i] = 0.0f;
+            const float *xg = xs + g * (GS + 4);
+            constexpr int TB = T < 4 ? T : 4;  // sub-blocks of 16 read per batch
 #pragma unroll
-                for (int t0 = 0; t0 < T; t0 += TB) {
-                    float4 vb[TB][4];
+            for (int t0 = 0; t0 < T; t0 += TB) {
+                float4 vb[TB][4];
 #pragma unroll
-                    for (int t = 0; t < TB; ++t)
+                for (int t = 0; t < TB; ++t)
 #pragma unroll
-                        for (int i4 = 0; i4 < 4; ++i4)
-                            vb[t][i4] = reinterpret_cast<const float4 *>(xg + 16 * (t0 + t))[i4];
-                    __builtin_amdgcn_sched_barrier(0);
+                    for (int i4 = 0; i4 < 4; ++i4)
+                        vb[t][i4] = reinterpret_cast<const float4 *>(xg + 16 * (t0 + t))[i4];
+                __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                    for (int t = 0; t < TB; ++t) {
+                for (int t = 0; t < TB; ++t) {
 #pragma unroll
-                        for (int i4 = 0; i4 < 4; ++i4) {
-                            const float4 v = vb[t][i4];
-                            P[4 * i4 + 0] = fmaf(v.x, v.x, P[4 * i4 + 0]);
-                            P[4 * i4 + 1] = fmaf(v.y, v.y, P[4 * i4 + 1]);
-                            P[4 * i4 + 2] = fmaf(v.z, v.z, P[4 * i4 + 2]);
-                            P[4 * i4 + 3] = fmaf(v.w, v.w, P[4 * i4 + 3]);
-                        }
+                    for (int i4 = 0; i4 < 4; ++i4) {
+                        const float4 v = vb[t][i4];
+                        Pc[4 * i4 + 0] = fmaf(v.x, v.x, Pc[4 * i4 + 0]);
+                        Pc[4 * i4 + 1] = fmaf(v.y, v.y, Pc[4 * i4 + 1]);
+                        Pc[4 * i4 + 2] = fmaf(v.z, v.z, Pc[4 * i4 + 2]);
+                        Pc[4 * i4 + 3] = fmaf(v.w, v.w, Pc[4 * i4 + 3]);
                     }
                 }
-                float V[8];
-#pragma unroll
-                for (int i = 0; i < 8; ++i) V[i] = P[i] + P[i + 8];
-                sumsq = tree8(V[0], V[1], V[2], V[3], V[4], V[5], V[6], V[7]);
             }
-            const float s = group_scale(sumsq, 1.0f / (float)GS);
-            const float inv = rcp_rn(s);
-            if (tg == 0) as_l[m * Kg + g] = s;
-            const float4 *xc4 = reinterpret_cast<const float4 *>(xs + xpos(16 * tid));
-            float4 xq[4];
+            float V[8];
 #pragma unroll
-            for (int q4 = 0; q4 < 4; ++q4) xq[q4] = xc4[q4];
+            for (int i = 0; i < 8; ++i) V[i] = Pc[i] + Pc[i + 8];
+            sumsq = tree8(V[0], V[1], V[2], V[3], V[4], V[5], V[6], V[7]);
+        }
+        const float s = group_scale(sumsq, 1.0f / (float)GS);
+        const float inv = rcp_rn(s);
+        if (tg == 0) as_l[m * Kg + g] = s;
+        const float4 *xc4 = reinterpret_cast<const float4 *>(xs + xpos(16 * tid));
+        float4 xq[4];
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) xq[q4] = xc4[q4];
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+            const float4 v = xq[q4];
+            qp[m][2 * q4] = quant_pair_finite(v.x * inv, v.y * inv);
+            qp[m][2 * q4 + 1] = quant_pair_finite(v.z * inv, v.w * inv);
+        }
+        if (__builtin_expect(!__builtin_isfinite(s), 0)) {  // a non-finite group (rare)
 #pragma unroll
             for (int q4 = 0; q4 < 4; ++q4) {
                 const float4 v = xq[q4];
-                qp[m][2 * q4] = quant_pair_finite(v.x * inv, v.y * inv);
-                qp[m][2 * q4 + 1] = quant_pair_finite(v.z * inv, v.w * inv);
-            }
-            if (__builtin_expect(!__builtin_isfinite(s), 0)) {  // a non-finite group (rare)
-#pragma unroll
-                for (int q4 = 0; q4 < 4; ++q4) {
-                    const float4 v = xq[q4];
-                    qp[m][2 * q4] = quant_pair(v.x * inv, v.y * inv);
-                    qp[m][2 * q4 + 1] = quant_pair(v.z * inv, v.w * inv);
-                }
+                qp[m][2 * q4] = quant_pair(v.x * inv, v.y * inv);
+                qp[m][2 * q4 + 1] = quant_pair(v.z * inv, v.w * inv);
             }
         }
+    };
+    if constexpr (P == 1) {
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) qp[m][j] = 0;
+            if (m >= M) continue;  // uniform: every thread skips together
+            const float4 *src = reinterpret_cast<const float4 *>(Ap + (size_t)m * K);
+            // four float4 per thread cover K/4 <= 4 * nthr (named registers; an
+            // array here ends up in scratch memory)
+            const int i0 = tid, i1 = tid + nthr, i2 = tid + 2 * nthr, i3 = tid + 3 * nthr;
+            const float4 x0 = src[i0 < K / 4 ? i0 : 0];
+            const float4 x1 = src[i1 < K / 4 ? i1 : 0];
+            const float4 x2 = src[i2 < K / 4 ? i2 : 0];
+            const float4 x3 = src[i3 < K / 4 ? i3 : 0];
+            // fused norm: this thread's 16 weight bytes and group scale
+            // (loaded unconditionally, from the activation row when there is no
+            // norm, so that no later wait depends on which loads were issued)
+            const int8_t *nwp = has_norm ? norm_w : reinterpret_cast<const int8_t *>(Ap);
+            const float *nsp = has_norm ? norm_s : Ap;
+            const u32x4 nw = *reinterpret_cast<const u32x4 *>(nwp + 16 * (act ? tid : 0));
+            const float nsc = nsp[act ? (16 * tid) / GS : 0];
+            if (m == 0) prefetch(resolve(tile));  // grid <= ntiles: every block has a tile
+            // keep the loads above ahead of the LDS stores below (the stores wait
+            // only for the activation loads, issued first); slots past K/4 exist
+            // (stage_words >= 16 * nthr + padding) and are never read
+            __builtin_amdgcn_sched_barrier(0);
+            float4 *xs4 = reinterpret_cast<float4 *>(xs);
+            xs4[xpos(4 * i0) / 4] = x0;
+            xs4[xpos(4 * i1) / 4] = x1;
+            xs4[xpos(4 * i2) / 4] = x2;
+            xs4[xpos(4 * i3) / 4] = x3;
+            if (has_norm) {
+                put4(i0, x0);
+                put4(i1, x1);
+                put4(i2, x2);
+                put4(i3, x3);
+            }
+            lds_barrier();
+            if (has_norm) {
+                norm_chain();
+                lds_barrier();
+                if (act) {
+                    // this thread's 16 elements: x = w * ((s_g * inv) * x)
+                    const float comb = nsc * s_norm_inv;
+                    const uint32_t wd[4] = {nw.x, nw.y, nw.z, nw.w};
+                    float4 *xc4 = reinterpret_cast<float4 *>(xs + xpos(16 * tid));
+#pragma unroll
+                    for (int q4 = 0; q4 < 4; ++q4) {
+                        float4 v = xc4[q4];
+                        const uint32_t w = wd[q4];
+                        v.x = (float)(int8_t)(w & 0xFF) * (comb * v.x);
+                        v.y = (float)(int8_t)((w >> 8) & 0xFF) * (comb * v.y);
+                        v.z = (float)(int8_t)((w >> 16) & 0xFF) * (comb * v.z);
+                        v.w = (float)(int8_t)(w >> 24) * (comb * v.w);
+                        xc4[q4] = v;
+                    }
+                }
+                lds_barrier();
+            }
+            if (act) quant_chunk(m);
+            lds_barrier();
+        }
+    } else {
+        // One activation row of K = 2048 over the block's 512 threads: thread
+        // bt holds float4 bt, so each group of 64 elements is one row of 16
+        // lanes (u = bt & 15 holds elements 4u .. 4u+3 of group bt >> 4) and
+        // the group is quantized in registers, with DPP moves inside the row.
+        const int bt = threadIdx.x;
+        const int8_t *nwp = has_norm ? norm_w : reinterpret_cast<const int8_t *>(Ap);
+        const float *nsp = has_norm ? norm_s : Ap;
+        float4 xv = reinterpret_cast<const float4 *>(Ap)[bt];
+        const uint32_t nw4 = *reinterpret_cast<const uint32_t *>(nwp + 4 * bt);  // norm weights of the 4
+        const float nsc4 = nsp[(4 * bt) / GS];
+        prefetch(resolve(tile));
+        __builtin_amdgcn_sched_barrier(0);
+        if (has_norm) {
+            put4(bt, xv);
+            lds_barrier();
+            norm_chain();
+            lds_barrier();
+            const float comb = nsc4 * s_norm_inv;  // x = w * ((s_g * inv) * x)
+            xv.x = (float)(int8_t)(nw4 & 0xFF) * (comb * xv.x);
+            xv.y = (float)(int8_t)((nw4 >> 8) & 0xFF) * (comb * xv.y);
+            xv.z = (float)(int8_t)((nw4 >> 16) & 0xFF) * (comb * xv.z);
+            xv.w = (float)(int8_t)(nw4 >> 24) * (comb * xv.w);
+        }
+        // The group's sum of squares in the reference order (as the T == 4
+        // quantizer): chain c = 4(u & 3) + k takes elements 16t + c, t = 0..3,
+        // whose step t is lane u = 4t + (u & 3). Each round every lane extends
+        // the chain value of lane u - 4 (row_shr:4; 0 into lanes 0..3), so
+        // after round t lanes 4t .. 4t+3 hold chains through step t, and lanes
+        // 12..15 end with the 16 chains. Then V[i] = P[i] + P[i+8] (lanes 12,
+        // 13 take lanes 14, 15: row_shl:2), lane 12 takes lane 13's half
+        // (row_shl:1), runs the fixed tree, and the row takes lane 12's sum
+        // (row_newbcast:12).
+#define Q3VL_DPPF(v, ctrl) \
+    __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), ctrl, 0xF, 0xF, false))
+        float c0 = fmaf(xv.x, xv.x, 0.0f), c1 = fmaf(xv.y, xv.y, 0.0f);
+        float c2 = fmaf(xv.z, xv.z, 0.0f), c3 = fmaf(xv.w, xv.w, 0.0f);
+#pragma unroll
+        for (int t = 1; t < 4; ++t) {
+            c0 = fmaf(xv.x, xv.x, Q3VL_DPPF(c0, 0x114));
+            c1 = fmaf(xv.y, xv.y, Q3VL_DPPF(c1, 0x114));
+            c2 = fmaf(xv.z, xv.z, Q3VL_DPPF(c2, 0x114));
+            c3 = fmaf(xv.w, xv.w, Q3VL_DPPF(c3, 0x114));
+        }
+        const float v0 = c0 + Q3VL_DPPF(c0, 0x102), v1 = c1 + Q3VL_DPPF(c1, 0x102);
+        const float v2 = c2 + Q3VL_DPPF(c2, 0x102), v3 = c3 + Q3VL_DPPF(c3, 0x102);
+        const float w0 = Q3VL_DPPF(v0, 0x101), w1 = Q3VL_DPPF(v1, 0x101);
+        const float w2 = Q3VL_DPPF(v2, 0x101), w3 = Q3VL_DPPF(v3, 0x101);
+        const float sumsq = Q3VL_DPPF(tree8(v0, v1, v2, v3, w0, w1, w2, w3), 0x15C);
+#undef Q3VL_DPPF
+        const float sg = group_scale(sumsq, 1.0f / (float)GS);
+        const float inv = rcp_rn(sg);
+        if ((bt & 15) == 0) as_l[bt >> 4] = sg;
+        uint32_t q0 = quant_pair_finite(xv.x * inv, xv.y * inv);
+        uint32_t q1 = quant_pair_finite(xv.z * inv, xv.w * inv);
+        if (__builtin_expect(!__builtin_isfinite(sg), 0)) {  // a non-finite group (rare)
+            q0 = quant_pair(xv.x * inv, xv.y * inv);
+            q1 = quant_pair(xv.z * inv, xv.w * inv);
+        }
+        reinterpret_cast<uint2 *>(qs)[bt] = make_uint2(q0, q1);
         lds_barrier();
+        // this thread's K-chunk (float4s 4*tid .. 4*tid+3)
+        const u32x4 *qs4 = reinterpret_cast<const u32x4 *>(qs) + 2 * tid;
+        const u32x4 qa = qs4[0], qb = qs4[1];
+        qp[0][0] = qa.x; qp[0][1] = qa.y; qp[0][2] = qa.z; qp[0][3] = qa.w;
+        qp[0][4] = qb.x; qp[0][5] = qb.y; qp[0][6] = qb.z; qp[0][7] = qb.w;
     }
 
     // Running argmax (argmax mode) of the block's tiles, in ascending row
@@ -471,7 +564,7 @@ __global__ __launch_bounds__(GEMV_MAX_THREADS) void gemv_kernel(GemvArgs a, int 
     int32_t bidx = -1;
 
     Tile cur = resolve(tile);
-    for (; tile < ntiles; tile += gridDim.x) {
+    for (; tile - sub < ntiles; tile += gridDim.x * P) {
         // ---- scales of the tile's rows -> LDS (values already in sv)
 #pragma unroll
         for (int j = 0; j < SPT; ++j) {
@@ -574,8 +667,8 @@ __global__ __launch_bounds__(GEMV_MAX_THREADS) void gemv_kernel(GemvArgs a, int 
 
         // ---- prefetch the next tile while this one finishes
         const Tile t = cur;
-        const int nxt = tile + gridDim.x;
-        if (nxt < ntiles) {
+        const int nxt = tile + gridDim.x * P;
+        if (nxt - sub < ntiles) {
             cur = resolve(nxt);
             prefetch(cur);
         }
@@ -698,7 +791,20 @@ __global__ __launch_bounds__(GEMV_MAX_THREADS) void gemv_kernel(GemvArgs a, int 
     // The running best of activation row m lives on lane m*R (general) or
     // lane 0 (lanes, M == 1).
     const int lead = LANES ? 0 : (tid % R == 0 && tid < M * R ? tid / R : -1);
-    if ((LANES ? tid == 0 : lead >= 0)) {
+    if constexpr (P > 1) {  // one activation row: the sub-groups' lane 0, combined
+        __shared__ float sbv[P];
+        __shared__ int32_t sbi[P];
+        if (tid == 0) {
+            sbv[sub] = best;
+            sbi[sub] = bidx;
+        }
+        lds_barrier();
+        if (threadIdx.x == 0) {
+            for (int q = 1; q < P; ++q) am_combine(best, bidx, sbv[q], sbi[q]);
+            a.part_val[blockIdx.x] = best;
+            a.part_idx[blockIdx.x] = bidx;
+        }
+    } else if ((LANES ? tid == 0 : lead >= 0)) {
         const int m = LANES ? 0 : lead;
         a.part_val[(size_t)blockIdx.x * M + m] = best;
         a.part_idx[(size_t)blockIdx.x * M + m] = bidx;
@@ -817,16 +923,34 @@ struct GridCache {
     }
 };
 
-template <int GS, int MR, bool LANES, int R, int KC = 0, int MD = MD_RUNTIME>
+// CU count per device, queried once.
+static hipError_t device_cus(int dev, int *cus) {
+    static std::mutex mu;
+    static std::vector<int> known;  // index: device, 0 = not queried
+    std::lock_guard<std::mutex> lk(mu);
+    if (dev >= (int)known.size()) known.resize(dev + 1, 0);
+    if (known[dev] <= 0) {
+        int n = 0;
+        hipError_t e = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev);
+        if (e != hipSuccess) return e;
+        known[dev] = n < 1 ? 1 : n;
+    }
+    *cus = known[dev];
+    return hipSuccess;
+}
+
+template <int GS, int MR, bool LANES, int R, int KC = 0, int MD = MD_RUNTIME, int P = 1>
 static hipError_t launch_gemv_t(const GemvArgs &a, int *grid_out, hipStream_t st) {
     const int K = a.K, Kg = K / GS;
     const int nthr = K / 16 > 64 ? K / 16 : 64;
+    if (P > 1 && (K != KC || a.M != 1)) return hipErrorInvalidValue;
     const int ld = group_ld(Kg);
     const int acc_words = (LANES ? 8 * R : MR * R) * ld;
     const int stage_need = 16 * nthr + 4 * (16 * nthr / GS) +
                            (a.norm_w ? 8 * norm_row_words(K, norm_seg(KC)) : 0);
-    const int stage_words = acc_words > stage_need ? acc_words : stage_need;
-    const size_t lds = (size_t)(stage_words + MR * Kg + R * ld + MR * R) * 4;
+    const int stage_words = P * acc_words > stage_need ? P * acc_words : stage_need;
+    const size_t lds =
+        (size_t)(stage_words + MR * Kg + (P > 1 ? 8 * nthr : 0) + P * (R * ld + MR * R)) * 4;
 
     int ntiles = 0;
     if (a.mode == GEMV_SWIGLU) {
@@ -840,21 +964,22 @@ static hipError_t launch_gemv_t(const GemvArgs &a, int *grid_out, hipStream_t st
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return e;
-    int grid = cache.find(dev, nthr, lds);
+    int grid = cache.find(dev, P * nthr, lds);
     if (grid <= 0) {
         int cus = 0, occ = 0;
         e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
         if (e != hipSuccess) return e;
-        e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, gemv_kernel<GS, MR, LANES, R, KC, MD>, nthr, lds);
+        e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, gemv_kernel<GS, MR, LANES, R, KC, MD, P>,
+                                                         P * nthr, lds);
         if (e != hipSuccess) return e;
         grid = cus * (occ < 1 ? 1 : occ);
-        cache.put(dev, nthr, lds, grid);
+        cache.put(dev, P * nthr, lds, grid);
     }
     if (grid > GEMV_MAX_GRID) grid = GEMV_MAX_GRID;  // argmax partials reserved per launch
-    if (grid > ntiles) grid = ntiles;
+    if (grid > (ntiles + P - 1) / P) grid = (ntiles + P - 1) / P;
     if (grid < 1) grid = 1;
     if (grid_out) *grid_out = grid;
-    gemv_kernel<GS, MR, LANES, R, KC, MD><<<grid, nthr, lds, st>>>(a, ntiles);
+    gemv_kernel<GS, MR, LANES, R, KC, MD, P><<<grid, P * nthr, lds, st>>>(a, ntiles);
     return hipGetLastError();
 }
 
@@ -878,25 +1003,73 @@ static int lane_rows(const GemvArgs &a) {
 
 // The lane path with K fixed at compile time for the decode step's row
 // lengths at group size 64.
-template <int GS, int R, int KC>
+template <int GS, int R, int KC, int P = 1>
 static hipError_t launch_lanes_k(const GemvArgs &a, int *grid_out, hipStream_t st) {
-    if (a.mode == GEMV_SWIGLU && a.nseg == 2) return launch_gemv_t<GS, 1, true, R, KC, MD_SWIGLU>(a, grid_out, st);
-    if (a.mode == GEMV_ARGMAX && a.nseg == 1) return launch_gemv_t<GS, 1, true, R, KC, MD_ARGMAX1>(a, grid_out, st);
-    return launch_gemv_t<GS, 1, true, R, KC>(a, grid_out, st);
+    if (a.mode == GEMV_SWIGLU && a.nseg == 2) return launch_gemv_t<GS, 1, true, R, KC, MD_SWIGLU, P>(a, grid_out, st);
+    if (a.mode == GEMV_ARGMAX && a.nseg == 1) return launch_gemv_t<GS, 1, true, R, KC, MD_ARGMAX1, P>(a, grid_out, st);
+    return launch_gemv_t<GS, 1, true, R, KC, MD_RUNTIME, P>(a, grid_out, st);
 }
 
-template <int GS, int R>
+template <int GS, int R, int P = 1>
 static hipError_t launch_lanes(const GemvArgs &a, int *grid_out, hipStream_t st) {
     if constexpr (GS == 64) {
-        if (a.K == 2048) return launch_lanes_k<GS, R, 2048>(a, grid_out, st);
+        if (a.K == 2048) return launch_lanes_k<GS, R, 2048, P>(a, grid_out, st);
         if (a.K == 6144) return launch_lanes_k<GS, R, 6144>(a, grid_out, st);
     }
     return launch_gemv_t<GS, 1, true, R>(a, grid_out, st);
 }
 
+// Rows per tile when blocks work on kSubGroups tiles side by side (K = 2048,
+// group 64): the tile groups should spread evenly over the CUs, since a CU
+// left with one group more than the others sets the kernel's length. Of
+// 8, 4 and 2 rows, the largest whose rounding waste (group slots left idle
+// in the last round over the CUs) is within 5% of the smallest. Returns 0
+// when that leaves more than 4 groups per CU: blocks that loop over many
+// tiles are held back by the block-wide barriers between their tiles (the
+// sub-groups wait for each other's weights), and run one tile per block
+// instead. Measured at the decode shapes: q|k|v 4 rows (256 groups), o 2
+// (256), gate|up 4 (768) are 2-14% faster than one tile per block; lm_head
+// (4748 groups) was 14% slower inside the decode step.
+static int lane_rows_sub(const GemvArgs &a, int cus) {
+    auto tiles = [&](int r) {
+        if (a.mode == GEMV_SWIGLU) return (a.seg[0].N + r / 2 - 1) / (r / 2);
+        int t = 0;
+        for (int s = 0; s < a.nseg; ++s) t += (a.seg[s].N + r - 1) / r;
+        return t;
+    };
+    double waste[3];
+    const int rows[3] = {8, 4, 2};
+    double best = 1.0;
+    for (int i = 0; i < 3; ++i) {
+        const int groups = (tiles(rows[i]) + kSubGroups - 1) / kSubGroups;
+        const int slots = (groups + cus - 1) / cus * cus;
+        waste[i] = (double)(slots - groups) / slots;
+        best = waste[i] < best ? waste[i] : best;
+    }
+    for (int i = 0; i < 3; ++i) {
+        if (waste[i] <= best + 0.05) {
+            const int groups = (tiles(rows[i]) + kSubGroups - 1) / kSubGroups;
+            return groups > 4 * cus ? 0 : rows[i];
+        }
+    }
+    return 0;
+}
+
 template <int GS>
 static hipError_t launch_gemv_gs(const GemvArgs &a, bool lanes, int *grid_out, hipStream_t st) {
     if (lanes) {
+        if (GS == 64 && a.K == 2048) {
+            int dev = 0, cus = 0;
+            hipError_t e = hipGetDevice(&dev);
+            if (e == hipSuccess) e = device_cus(dev, &cus);
+            if (e != hipSuccess) return e;
+            switch (lane_rows_sub(a, cus)) {
+                case 2: return launch_lanes<GS, 2, kSubGroups>(a, grid_out, st);
+                case 4: return launch_lanes<GS, 4, kSubGroups>(a, grid_out, st);
+                case 8: return launch_lanes<GS, 8, kSubGroups>(a, grid_out, st);
+                default: break;  // one tile per block
+            }
+        }
         switch (lane_rows(a)) {
             case 2: return launch_lanes<GS, 2>(a, grid_out, st);
             case 4: return launch_lanes<GS, 4>(a, grid_out, st);

@@ -76,7 +76,10 @@ def test_quantize_ties_round_half_even(orc):
 # --------------------------------------------------------------- linear paths
 LANE = [(1, 1024, 1024, 64), (1, 6144, 2048, 64), (1, 2048, 6144, 64), (1, 4096, 2048, 64),
         (1, 1024, 2048, 16), (1, 1024, 2048, 32), (1, 1024, 2048, 128), (1, 1024, 4096, 256),
-        (1, 1028, 1024, 64), (1, 1031, 1024, 64), (1, 70000, 1024, 64)]
+        (1, 1028, 1024, 64), (1, 1031, 1024, 64), (1, 70000, 1024, 64),
+        # K = 2048, group 64 runs blocks of several row tiles: a last tile
+        # with one valid row, sub-groups past the last tile, grid strides
+        (1, 1029, 2048, 64), (1, 70001, 2048, 64), (1, 2050, 2048, 64)]
 GENERAL = [(1, 512, 2048, 64), (1, 2048, 512, 64), (2, 256, 512, 64), (3, 1000, 2048, 64),
            (5, 1028, 1024, 32), (8, 1000, 2048, 64), (8, 384, 6144, 64), (4, 77, 1024, 128),
            (6, 96, 256, 16), (2, 64, 1024, 256),
@@ -206,7 +209,8 @@ def test_extreme_activation_groups(orc, M):
 
 # -------------------------------------------------------------- fused consumers
 @pytest.mark.parametrize("M,N,K", [(1, 6144, 2048), (1, 1024, 1024), (4, 512, 1024), (64, 512, 1024),
-                                   (512, 768, 2048), (512, 6144, 2048), (300, 8200, 1024)])
+                                   (512, 768, 2048), (512, 6144, 2048), (300, 8200, 1024),
+                                   (1, 1030, 2048), (1, 1027, 2048)])
 def test_swiglu_fused_parity(orc, M, N, K):
     gs = 64
     A, Wg, Sg = make_case(100 + M, M, N, K, gs)
@@ -264,6 +268,28 @@ def test_lm_head_argmax_parity(orc, M):
     np.testing.assert_array_equal(ids, ids_ref)
     ids2 = host(q.lm_head_argmax(dA, dW, dS, gs))  # logits not stored
     np.testing.assert_array_equal(ids2, ids_ref)
+
+
+@pytest.mark.parametrize("V,off", [(70001, 9), (4099, 5), (151936, 16)])
+def test_lm_head_argmax_lane_ties_across_tiles(orc, V, off):
+    """M = 1 at K = 2048: the winning row copied `off` rows lower (another
+    row tile, worked on by another sub-group of the same block or by another
+    block) and 3 rows higher; the lowest index must win. V = 70001 and 4099
+    leave a last tile with few valid rows and sub-groups past the end."""
+    K, gs = 2048, 64
+    A, W, S = make_case(400 + off, 1, V, K, gs)
+    top = int(orc.argmax_rows(orc.linear(A, W, S, gs))[0])
+    lo = top - off if top >= off else top + 2 * off
+    for r in (lo, min(top + 3, V - 1)):
+        W[r] = W[top]
+        S[r] = S[top]
+    logits_ref = orc.linear(A, W, S, gs)
+    ids_ref = orc.argmax_rows(logits_ref)
+    assert logits_ref[0, lo] == logits_ref[0, top]
+    logits = torch.empty((1, V), dtype=torch.float32, device="cuda")
+    ids = host(q.lm_head_argmax(dev(A), dev(W), dev(S), gs, logits=logits))
+    assert_bits_equal(host(logits), logits_ref, "logits")
+    np.testing.assert_array_equal(ids, ids_ref)
 
 
 @pytest.mark.parametrize("M,V,K", [(12, 5000, 1024), (40, 33000, 2048), (6, 70001, 1024),
@@ -335,6 +361,11 @@ def test_multi_matches_separate(orc):
     outs = q.linear_i8_multi(dev(A), [dev(Wq), dev(Wk), dev(Wv)], [dev(Sq), dev(Sk), dev(Sv)], gs)
     for o, (W, S) in zip(outs, [(Wq, Sq), (Wk, Sk), (Wv, Sv)]):
         assert_bits_equal(host(o), orc.linear(A, W, S, gs), "multi")
+    # ragged segments (row tiles that straddle no segment end)
+    segs = [make_case(5 + i, 1, n, K, gs)[1:] for i, n in enumerate((1030, 1027, 1025))]
+    outs = q.linear_i8_multi(dev(A), [dev(W) for W, _ in segs], [dev(S) for _, S in segs], gs)
+    for o, (W, S) in zip(outs, segs):
+        assert_bits_equal(host(o), orc.linear(A, W, S, gs), "multi ragged")
     # mixed paths (N < 1024 segment with M=1) fall back to separate launches
     _, Ws, Ss = make_case(4, 1, 512, K, gs)
     outs = q.linear_i8_multi(dev(A), [dev(Wq), dev(Ws)], [dev(Sq), dev(Ss)], gs)
