@@ -121,7 +121,9 @@ __global__ __launch_bounds__(GEMV_MAX_THREADS) void gemv_kernel(GemvArgs a, int 
     const int M = a.M;
     // thread index within the sub-group (the K-chunk it owns) and sub-group
     const int tid = P > 1 ? (int)(threadIdx.x & 127) : (int)threadIdx.x;
-    const int sub = P > 1 ? (int)(threadIdx.x >> 7) : 0;
+    // (wave-uniform: a sub-group is two whole waves; readfirstlane keeps the
+    // sub-group's tile, segment and row checks in scalar registers)
+    const int sub = P > 1 ? __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 7)) : 0;
     const int nthr = KC ? (KC / 16 > 64 ? KC / 16 : 64) : (int)blockDim.x;  // max(K/16, 64)
     const int nchunk = K / 16;
     const bool act = tid < nchunk;   // owns a 16-byte K-chunk
@@ -592,7 +594,7 @@ __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), c
                 constexpr int W = 8 / T;
                 int32_t p[8];
 #pragma unroll
-                for (int j = 0; j < 8; ++j) p[j] = dot2(qp[0][j], wp[j], 0);
+                for (int j = 0; j < 8; ++j) p[j] = dot2_z(qp[0][j], wp[j]);
                 scatter_sums<T>(p, tg);
                 if (act) {
 #pragma unroll
@@ -608,7 +610,7 @@ __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), c
             } else if constexpr (LANES) {
                 int32_t p[8];
 #pragma unroll
-                for (int j = 0; j < 8; ++j) p[j] = run_sum<T>(dot2(qp[0][j], wp[j], 0));
+                for (int j = 0; j < 8; ++j) p[j] = run_sum<T>(dot2_z(qp[0][j], wp[j]));
                 // every thread of the group holds all 8 sums: threads 0..7
                 // of the group write one each
                 if (act && tg < 8) {

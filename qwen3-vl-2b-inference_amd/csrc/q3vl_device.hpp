@@ -160,6 +160,18 @@ Q3VL_INLINE int32_t dot2(uint32_t a, uint32_t b, int32_t c) {
                                   __builtin_bit_cast(short2_t, b), c, false);
 }
 
+// dot2(a, b, 0) as one VOP3P instruction with an inline 0 accumulator (the
+// compiler picks the two-operand form, whose accumulator a move must zero).
+Q3VL_INLINE int32_t dot2_z(uint32_t a, uint32_t b) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    int32_t r;
+    asm("v_dot2_i32_i16 %0, %1, %2, 0" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+#else
+    return dot2(a, b, 0);
+#endif
+}
+
 // DPP sums inside a quad of lanes (row_mask/bank_mask all lanes).
 // quad_perm [1,0,3,2] = 0xB1 (xor 1), [2,3,0,1] = 0x4E (xor 2).
 Q3VL_INLINE int32_t dpp_xor1(int32_t v) {
