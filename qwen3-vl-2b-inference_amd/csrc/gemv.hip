@@ -709,10 +709,16 @@ __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), c
                     }
                     for (; gg < Kg; ++gg) c = fmaf((float)Lr[gg], scr[gg], c);
                 }
-                // add_reduce_mm_256 over the row's 8 lanes (i8:219-222).
-                c = c + __shfl_xor(c, 4, 8);
-                c = c + __shfl_xor(c, 1, 8);
-                c = c + __shfl_xor(c, 2, 8);
+                // add_reduce_mm_256 over the row's 8 lanes (i8:219-222):
+                // lane j = 0 ends with ((c0+c4) + (c1+c5)) + ((c2+c6) + (c3+c7)),
+                // taking lane j+4, then j+1, then j+2 (DPP row shifts; the
+                // other lanes' values are not used)
+#define Q3VL_SHL(v, n) \
+    __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x100 + (n), 0xF, 0xF, false))
+                c = c + Q3VL_SHL(c, 4);
+                c = c + Q3VL_SHL(c, 1);
+                c = c + Q3VL_SHL(c, 2);
+#undef Q3VL_SHL
                 y = c;
                 yr = r;
                 yvalid = (j == 0) && row_ok(t, r);
@@ -753,13 +759,20 @@ __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), c
                 *dst = a.accumulate ? *dst + y : y;  // add_vector: to[i] += from[i]
             }
         } else if (swg) {
-            if (yvalid) ybuf[ym * R + yr] = y;
-            lds_barrier();
-            if (tid < M * HALF) {
-                const int m = tid / HALF, r = tid - (tid / HALF) * HALF;
-                if (row_ok(t, r))
-                    sr.Y0[(size_t)m * t.tN + row_n(t, r)] =
-                        silu_mul(ybuf[m * R + r], ybuf[m * R + r + HALF]);
+            if constexpr (LANES) {
+                // the up row of gate row r is row r + HALF, whose sum sits
+                // 8 * HALF lanes above (all in the first wave: 8R <= 64)
+                const float up = __shfl_down(y, 8 * HALF);
+                if (yvalid && yr < HALF) sr.Y0[row_n(t, yr)] = silu_mul(y, up);
+            } else {
+                if (yvalid) ybuf[ym * R + yr] = y;
+                lds_barrier();
+                if (tid < M * HALF) {
+                    const int m = tid / HALF, r = tid - (tid / HALF) * HALF;
+                    if (row_ok(t, r))
+                        sr.Y0[(size_t)m * t.tN + row_n(t, r)] =
+                            silu_mul(ybuf[m * R + r], ybuf[m * R + r + HALF]);
+                }
             }
         } else {  // GEMV_ARGMAX, in registers of the wave that holds y
             if (yvalid && sr.Y0) sr.Y0[(size_t)ym * t.tN + row_n(t, yr)] = y;
