@@ -667,10 +667,13 @@ __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), c
             }
         }
 
-        // ---- prefetch the next tile while this one finishes
+        // ---- prefetch the next tile while this one finishes. (Sub-group
+        // blocks issue it after the epilogue instead: there the weight stream
+        // fills the memory queues, a wave issuing loads waits for queue room,
+        // and that wait would hold back this tile's chains and stores.)
         const Tile t = cur;
         const int nxt = tile + gridDim.x * P;
-        if (nxt - sub < ntiles) {
+        if (P == 1 && nxt < ntiles) {
             cur = resolve(nxt);
             prefetch(cur);
         }
@@ -795,6 +798,10 @@ __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), c
                 best = cv;
                 bidx = ci;
             }
+        }
+        if (P > 1 && nxt - sub < ntiles) {
+            cur = resolve(nxt);
+            prefetch(cur);
         }
         lds_barrier();
     }
