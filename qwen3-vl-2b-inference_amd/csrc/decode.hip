@@ -498,19 +498,74 @@ __global__ __launch_bounds__(ATT_HD) void attn_combine_kernel(AttnArgs a) {
 //   p_t = e_t * (float)(1/sum)   (all zero if M or sum is not finite/positive),
 //   out[d] = fma chain over t = 0..pos of p_t * v_t[d].
 // The chain is inherently sequential (one dependent FMA per position), so
-// everything else is arranged around it. Loads are issued at entry in the
-// order they are needed (chunk maxima, scores, then the first V chunk), so the
-// softmax runs while V is still arriving. V is widened to fp32 into LDS,
-// transposed ([d][t]); p is formed in LDS before the chains start; the chains
-// read 32 positions ahead with the reads spread between the FMAs. e also
-// lives lane-major (row j holds e_j, e_{j+8}, ...) so the 8 summing lanes
-// read contiguous 16-byte words.
+// everything else is arranged around it. Loads are issued at entry (the
+// position first, then chunk maxima, scores and the first V chunk, in order
+// of use), so the softmax runs while V is still arriving. V is widened to
+// fp32 into LDS, transposed ([d][t]) with 16-byte row writes of 4 positions;
+// later chunks are loaded by waves 2 and 3 while the chain runs, so the
+// chain wave issues no loads. The chains read 64 positions ahead with the
+// reads spread between the FMAs. e also lives lane-major (row j holds e_j,
+// e_{j+8}, ...), which the denominator's segmented sums read.
 constexpr int PV_D = 16;
 constexpr int PV_TC = 1024;
 constexpr int PV_THREADS = 256;
 constexpr int PV_RS = PV_TC + 4;                    // floats per LDS row of vt
-constexpr int PV_ITEMS = PV_TC * (PV_D / 8) / PV_THREADS;  // 16-byte V pieces per thread
+// chunk 0 is staged by all waves (PV_Q0 quads a thread), later chunks by
+// waves 2 and 3 (PV_QN quads a thread)
+constexpr int PV_Q0 = PV_TC * (PV_D / 8) / PV_THREADS / 4;
+constexpr int PV_QN = 2 * PV_Q0;
+static_assert(4 * (PV_THREADS / 2) * PV_Q0 == PV_TC && 4 * (PV_THREADS / 4) * PV_QN == PV_TC,
+              "the staging quads cover the chunk");
 constexpr int PV_SREG = 4;  // float4 score groups held in registers per head (4096 positions)
+
+// V staging: thread (vsg, vb) of a staging group holds the 8-dim half vsg
+// of the NQ quads of positions 4*(vb + QSTR*q) + i (item 4q + i) of a
+// chunk, so each of its dims becomes one 16-byte LDS row write. Rows are
+// clamped into the cache when loaded.
+template <int NQ, int QSTR>
+__device__ __forceinline__ void pv_load(u32x4 *vr, const uint16_t *vc, int t0, int S, int vsg, int vb) {
+#pragma unroll
+    for (int it = 0; it < 4 * NQ; ++it) {
+        const int t = t0 + 4 * (vb + QSTR * (it >> 2)) + (it & 3);
+        vr[it] = *reinterpret_cast<const u32x4 *>(vc + (size_t)min(t, S - 1) * ATT_HD + vsg * 8);
+    }
+}
+// Widens the staged V to fp32 rows vt[d][t]. Rows past pos are stored as
+// zeros (their steps then add exact +0, even where the row at pos holds an
+// infinity); quads at or past lim (the chunk-relative end of what the chains
+// read, a multiple of 64) are not stored at all. (The chunk without rows
+// past pos takes a loop of its own, free of selects.)
+template <int NQ, int QSTR>
+__device__ __forceinline__ void pv_store(float *vt, const u32x4 *vr, int vsg, int vb, int t0, int lim, int pos) {
+    auto quad = [&](int q, bool masked) {
+        const int p0 = 4 * (vb + QSTR * q);
+        if (p0 >= lim) return;
+        float4 f[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const u32x4 v = vr[4 * q + i];
+            const bool past = masked && t0 + p0 + i > pos;
+            const uint32_t w[4] = {past ? 0u : v.x, past ? 0u : v.y, past ? 0u : v.z, past ? 0u : v.w};
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const float x = h2f((uint16_t)(w[k >> 1] >> (16 * (k & 1))));
+                if (i == 0) f[k].x = x;
+                if (i == 1) f[k].y = x;
+                if (i == 2) f[k].z = x;
+                if (i == 3) f[k].w = x;
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < 8; ++k) *reinterpret_cast<float4 *>(vt + (vsg * 8 + k) * PV_RS + p0) = f[k];
+    };
+    if (t0 + PV_TC <= pos + 1) {
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) quad(q, false);
+    } else {
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) quad(q, true);
+    }
+}
 
 // Lane-major e rows hold max_seq/8 terms rounded up to a multiple of 32 (the
 // summing batch), plus 4 floats of padding against bank conflicts.
@@ -531,10 +586,15 @@ __global__ __launch_bounds__(PV_THREADS) void attn_softmax_pv_kernel(AttnArgs a)
     const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63;
     const uint16_t *vc = a.v_cache + ((size_t)a.layer * a.kv_heads + kvh) * S * ATT_HD + db * PV_D;
 
-    // ---- entry loads, in order of use, all issued before `pos` is known
-    // (their latency overlaps its own). Every load is unconditional, with
-    // indices clamped into the buffers, so no wait depends on which were
-    // issued; values past the context are masked once pos is known.
+    // ---- entry loads. The position's scalar load goes first (the vector
+    // loads below can wait at issue for queue room, and it must not wait
+    // behind them); the others follow in order of use, all issued before
+    // `pos` is known (their latency overlaps its own). Every load is
+    // unconditional, with indices clamped into the buffers, so no wait
+    // depends on which were issued; values past the context are masked once
+    // pos is known.
+    const int pos = *a.pos;
+    __builtin_amdgcn_sched_barrier(0);
     // chunk maxima: wave hh < kvm, lane c (one pass covers 4096 positions)
     const int wh = min(wid, kvm - 1);
     const float cm = a.cmax[(kvh * kvm + wh) * a.max_chunks + min(lane, a.max_chunks - 1)];
@@ -546,22 +606,18 @@ __global__ __launch_bounds__(PV_THREADS) void attn_softmax_pv_kernel(AttnArgs a)
 #pragma unroll
         for (int k = 0; k < PV_SREG; ++k) sreg[hh][k] = sc[min(tid + PV_THREADS * k, S / 4 - 1)];
     }
-    // V chunk loads: item -> (position t, 8-dim segment sg), the two segments of
-    // a row on adjacent lanes (a wave load covers 32 rows x 32 bytes); rows
-    // clamped into the cache (rows past pos are zeroed when stored)
-    u32x4 vr[PV_ITEMS];
-    auto load_chunk = [&](int t0) {
-#pragma unroll
-        for (int it = 0; it < PV_ITEMS; ++it) {
-            const int item = it * PV_THREADS + tid, sg = item & 1, t = t0 + (item >> 1);
-            vr[it] = *reinterpret_cast<const u32x4 *>(vc + (size_t)min(t, S - 1) * ATT_HD + sg * 8);
-        }
-    };
+    // V chunk 0: every thread loads its share at entry (thread tid: vsg =
+    // tid & 1, vb = tid >> 1, quads vb and vb + 128) and widens it into LDS
+    // after its softmax work. Later chunks: waves 2 and 3 (staging thread
+    // tid & 127: vb = (tid & 127) >> 1, quads vb + 64q) load them while the
+    // chain runs on the previous one, so the chain wave issues no loads.
+    u32x4 vr0[4 * PV_Q0], vrn[4 * PV_QN];
+    const int vsg = tid & 1;
+    const bool stager = __builtin_amdgcn_readfirstlane(wid) >= 2;  // wave-uniform
     __builtin_amdgcn_sched_barrier(0);
-    load_chunk(0);
+    pv_load<PV_Q0, PV_THREADS / 2>(vr0, vc, 0, S, vsg, tid >> 1);
     __builtin_amdgcn_sched_barrier(0);
 
-    const int pos = *a.pos;
     if (pos < 0 || pos >= S) {  // no cache row for it: NaN outputs
         if (wid == 0 && (lane >> 4) < kvm)
             a.out[(kvh * kvm + (lane >> 4)) * ATT_HD + db * PV_D + (lane & 15)] = __builtin_nanf("");
@@ -571,20 +627,7 @@ __global__ __launch_bounds__(PV_THREADS) void attn_softmax_pv_kernel(AttnArgs a)
     const int nb = n & ~7;
     const int nch = (n + ATT_CH - 1) / ATT_CH;
     const int kreg = min(PV_SREG, (n + 4 * PV_THREADS - 1) / (4 * PV_THREADS));  // uniform
-    // rows past pos are stored as zeros (their steps then add exact +0, even
-    // where the row at pos holds an infinity)
-    auto store_chunk = [&](int t0) {
-#pragma unroll
-        for (int it = 0; it < PV_ITEMS; ++it) {
-            const int item = it * PV_THREADS + tid, sg = item & 1, t = item >> 1;
-            const bool past = t0 + t > pos;
-            const uint32_t w[4] = {past ? 0u : vr[it].x, past ? 0u : vr[it].y, past ? 0u : vr[it].z,
-                                   past ? 0u : vr[it].w};
-#pragma unroll
-            for (int i = 0; i < 8; ++i)
-                vt[(sg * 8 + i) * PV_RS + t] = h2f((uint16_t)(w[i >> 1] >> (16 * (i & 1))));
-        }
-    };
+    auto chunk_lim = [&](int t0) { return (min(PV_TC, n - t0) + 63) & ~63; };
 
     // ---- M per head from the chunk maxima (beyond one pass: loop)
     if (wid < kvm) {
@@ -634,59 +677,49 @@ __global__ __launch_bounds__(PV_THREADS) void attn_softmax_pv_kernel(AttnArgs a)
         for (int i = tid + PV_THREADS * PV_SREG; 4 * i < n; i += PV_THREADS) put4(4 * i, sc[i]);
     }
     lds_barrier();
-    // ---- sums and the fp32 inverse, lanes 0..7 of one wave per head; the
-    // other waves widen V chunk 0 into LDS meanwhile
+    // ---- sums and the fp32 inverse, one wave per head; waves 2 and 3 widen
+    // V chunk 0 into LDS meanwhile. Lane sum l (the sequential fp32 sum over
+    // t = l mod 8) is cut into segments of 32 terms; in a pass over 256 terms
+    // lane 8l+s holds segment s of sum l in registers. Every lane adds its
+    // segment's terms in each round, and a DPP row shift hands each lane's
+    // value to the next segment's lane between rounds (row_ror:9 from the
+    // last lane of one pass to the first of the next), so lane 8l+s carries
+    // sum l through segment s in round s: the same adds in the same order as
+    // one lane summing the whole row, with no LDS read between them.
     if (wid < kvm) {
-        const float *row = et + wid * 8 * ets + (lane & 7) * ets;
-        const int cnt = ((nb >> 3) + 31) & ~31;  // terms per lane, zero-padded
+        const int cnt = ((nb >> 3) + 31) & ~31;  // terms per lane sum, zero-padded
+        const float *rowl = et + wid * 8 * ets + (lane >> 3) * ets + 32 * (lane & 7);
         const float *eh = e + wid * S;
         // the tail e_nb .. e_pos (at most 7), one per lane
         const float tl = lane < n - nb ? eh[nb + lane] : 0.0f;
-        float ls = 0.0f;
-        if (lane < 8 && cnt > 0) {
-            float4 A[8], B[8];
-            auto ld = [&](float4 *D, int i) {
+        float acc = 0.0f;
+        int last = 7;  // segment lane that ends with the sums
+        for (int p0 = 0; p0 < cnt; p0 += 256) {
+            const int nr = min(8, (cnt - p0) >> 5);  // segments in this pass
+            // (segments past cnt read LDS words whose sums are never kept)
+            float4 X[8];
 #pragma unroll
-                for (int u = 0; u < 8; ++u) D[u] = *reinterpret_cast<const float4 *>(row + i + 4 * u);
-            };
-            auto add = [&](const float4 *D) {
+            for (int u = 0; u < 8; ++u) X[u] = reinterpret_cast<const float4 *>(rowl + p0)[u];
+            if (p0 > 0)
+                acc = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                          0, __builtin_bit_cast(int, acc), 0x129, 0xF, 0xF, false));
+            for (int r = 0; r < nr; ++r) {
+                if (r > 0)  // row_shr:1 (lane i takes lane i-1 inside each row of 16)
+                    acc = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                              0, __builtin_bit_cast(int, acc), 0x111, 0xF, 0xF, false));
 #pragma unroll
                 for (int u = 0; u < 8; ++u) {
-                    ls = ls + D[u].x;
-                    ls = ls + D[u].y;
-                    ls = ls + D[u].z;
-                    ls = ls + D[u].w;
+                    acc = acc + X[u].x;
+                    acc = acc + X[u].y;
+                    acc = acc + X[u].z;
+                    acc = acc + X[u].w;
                 }
-            };
-            ld(A, 0);
-            int i = 0;
-            for (; i + 64 <= cnt; i += 64) {
-                lgkm_wait0();  // A has landed; B's reads go out between A's adds
-                __builtin_amdgcn_sched_barrier(0);
-                ld(B, i + 32);
-                add(A);
-#pragma unroll
-                for (int g = 0; g < 8; ++g) {
-                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
-                    __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // four adds
-                }
-                __builtin_amdgcn_sched_barrier(0);
-                lgkm_wait0();
-                __builtin_amdgcn_sched_barrier(0);
-                ld(A, min(i + 64, cnt - 32));
-                add(B);
-#pragma unroll
-                for (int g = 0; g < 8; ++g) {
-                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
-                    __builtin_amdgcn_sched_group_barrier(0x002, 4, 1);
-                }
-                __builtin_amdgcn_sched_barrier(0);
             }
-            if (i < cnt) add(A);  // one batch of 32 left
+            last = nr - 1;
         }
         double sum = 0.0;
 #pragma unroll
-        for (int l = 0; l < 8; ++l) sum += (double)readlane_f(ls, l);
+        for (int l = 0; l < 8; ++l) sum += (double)readlane_f(acc, 8 * l + last);  // lane sum l
 #pragma unroll
         for (int l = 0; l < 7; ++l)
             if (l < n - nb) sum += (double)readlane_f(tl, l);
@@ -694,7 +727,7 @@ __global__ __launch_bounds__(PV_THREADS) void attn_softmax_pv_kernel(AttnArgs a)
         const float inv = ok ? (float)(1.0 / sum) : 0.0f;
         if (lane == 0) hinv[wid] = inv;
     }
-    store_chunk(0);  // V chunk 0 (its loads were issued at entry)
+    pv_store<PV_Q0, PV_THREADS / 2>(vt, vr0, vsg, tid >> 1, 0, chunk_lim(0), pos);  // V chunk 0
 
     // ---- value-weighted sums. Wave 0 runs the chains: row r of 16 lanes is
     // query head r, lane d of the row output dim db*PV_D + d. Per batch of 64
@@ -708,10 +741,10 @@ __global__ __launch_bounds__(PV_THREADS) void attn_softmax_pv_kernel(AttnArgs a)
     for (int t0 = 0; t0 < n; t0 += PV_TC) {
         if (t0 > 0) {
             lds_barrier();  // previous chains done with vt
-            store_chunk(t0);
+            if (stager) pv_store<PV_QN, PV_THREADS / 4>(vt, vrn, vsg, (tid & 127) >> 1, t0, chunk_lim(t0), pos);
         }
         lds_barrier();      // vt (and inv) ready
-        if (t0 + PV_TC < n) load_chunk(t0 + PV_TC);
+        if (stager && t0 + PV_TC < n) pv_load<PV_QN, PV_THREADS / 4>(vrn, vc, t0 + PV_TC, S, vsg, (tid & 127) >> 1);
         if (chain) {
             const float invh = hinv[hrow];
             const float *eph = e + hrow * S + t0;
