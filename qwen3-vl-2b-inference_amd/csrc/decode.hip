@@ -101,6 +101,20 @@ __device__ __forceinline__ float readlane_f(float v, int lane) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
 }
 
+// Maximum over the 64 lanes (fmaxf, so NaN lanes drop out), wave-uniform:
+// quad swaps, then the mirror inside 8 and 16 lanes (each lane ends with the
+// maximum of its row of 16), then the four rows' lane 0.
+__device__ __forceinline__ float wave_max(float v) {
+#define Q3VL_DPPM(x, ctrl) \
+    __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), ctrl, 0xF, 0xF, false))
+    v = fmaxf(v, Q3VL_DPPM(v, 0xB1));   // quad_perm [1,0,3,2]
+    v = fmaxf(v, Q3VL_DPPM(v, 0x4E));   // quad_perm [2,3,0,1]
+    v = fmaxf(v, Q3VL_DPPM(v, 0x141));  // row_half_mirror
+    v = fmaxf(v, Q3VL_DPPM(v, 0x140));  // row_mirror
+#undef Q3VL_DPPM
+    return fmaxf(fmaxf(readlane_f(v, 0), readlane_f(v, 16)), fmaxf(readlane_f(v, 32), readlane_f(v, 48)));
+}
+
 // Left-to-right fold of the 8 lane accumulators held by lanes 0..7:
 // ((c0 + c1) + c2) + ... + c7; wave-uniform result.
 __device__ __forceinline__ float fold8_lanes(float c) {
@@ -204,7 +218,6 @@ template <bool PAR>
 __global__ __launch_bounds__(ATT_THREADS) void attn_scores_kernel(AttnArgs a) {
     __shared__ float qsh[3][ATT_HD];
     __shared__ uint16_t ksh[ATT_CH * ATT_KSTR];
-    __shared__ __align__(16) uint16_t knew[ATT_HD];
     __shared__ __align__(16) uint16_t vnew[PAR ? ATT_HD : 1];
     __shared__ __align__(16) uint32_t vsh[PAR ? ATT_CH / 2 * ATT_HD : 1];  // [t/2][d]: (v_2r[d], v_2r+1[d])
     __shared__ __align__(16) float esh[PAR ? 3 : 1][ATT_CH];
@@ -224,6 +237,10 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_scores_kernel(AttnArgs a) {
     // clamped into the cache -- rows at or past the context are replaced
     // when staged. vmcnt retires in order, so the norms wait only for their
     // own loads.
+    // (the position's scalar load goes first: vector loads can wait at
+    // issue for queue room, and it must not wait behind them)
+    const int pos = *a.pos;
+    __builtin_amdgcn_sched_barrier(0);
     NormRopeIn nri{};
     float vlo = 0.0f, vhi = 0.0f;
     if (q_wave || k_wave) {
@@ -261,7 +278,6 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_scores_kernel(AttnArgs a) {
         }
     }
 
-    const int pos = *a.pos;
     if (pos < 0 || pos >= S) return;  // no cache row for it: nothing is touched
     const int n = pos + 1;
     if (t0 >= n) return;  // uniform: chunk past the context
@@ -284,8 +300,9 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_scores_kernel(AttnArgs a) {
         const uint16_t l16 = f2h(lo), h16 = f2h(hi);
         kc[(size_t)pos * ATT_HD + lane] = l16;
         kc[(size_t)pos * ATT_HD + 64 + lane] = h16;
-        knew[lane] = l16;
-        knew[lane + 64] = h16;
+        // row pos of the key tile, written here (the staging below skips it)
+        ksh[(pos - t0) * ATT_KSTR + lane] = l16;
+        ksh[(pos - t0) * ATT_KSTR + 64 + lane] = h16;
         const uint16_t vl16 = f2h(vlo), vh16 = f2h(vhi);
         vc[(size_t)pos * ATT_HD + lane] = vl16;
         vc[(size_t)pos * ATT_HD + 64 + lane] = vh16;
@@ -294,17 +311,16 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_scores_kernel(AttnArgs a) {
             vnew[lane + 64] = vh16;
         }
     }
-    lds_barrier();  // knew, vnew
 #pragma unroll
     for (int it = 0; it < ATT_KITEMS; ++it) {
         const int idx = it * ATT_THREADS + tid, r = idx >> 4, c8 = idx & 15;
         const int t = t0 + r;
         u32x4 v = kr[it];
         if (t >= n) v = (u32x4){0u, 0u, 0u, 0u};
-        else if (t == pos) v = *reinterpret_cast<const u32x4 *>(knew + c8 * 8);
-        *reinterpret_cast<u32x4 *>(ksh + r * ATT_KSTR + c8 * 8) = v;
+        if (t != pos) *reinterpret_cast<u32x4 *>(ksh + r * ATT_KSTR + c8 * 8) = v;
     }
     if constexpr (PAR) {
+        lds_barrier();  // vnew
         // pairs (v_2rp[d], v_2rp+1[d]); rows past the context as zeros, row
         // pos from vnew
 #pragma unroll
@@ -361,9 +377,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_scores_kernel(AttnArgs a) {
         score = dot * a.inv_sqrt_d;
         a.scores[(size_t)h * a.max_seq + t] = score;
     }
-    float m = score;
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    const float m = wave_max(score);
     if (lane == 0) a.cmax[h * a.max_chunks + ch] = m;
     if constexpr (PAR) {
         const float e = (lane < rows && score > -INFINITY && __builtin_isfinite(m)) ? exp256(score - m) : 0.0f;
