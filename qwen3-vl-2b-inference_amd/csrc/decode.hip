@@ -38,32 +38,19 @@ __device__ __forceinline__ float exp256(float x) {
 }
 
 __device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
-// fp32 -> fp16 bits, round to nearest even, computed on the integer image.
-// A plain (_Float16) conversion lets the compiler fuse it with the fmaf that
-// produced the value (v_fma_mixlo_f16 rounds the exact result once, straight
-// to fp16), which differs from the reference's fp32 result rounded to fp16
-// whenever that result lies exactly halfway between two fp16 values.
+// fp32 -> fp16 bits, round to nearest even (NaN -> sign | 0x7E00), as one
+// v_cvt_f16_f32 on the fp32 value. A plain (_Float16) conversion lets the
+// compiler fuse it with the fmaf that produced the value (v_fma_mixlo_f16
+// rounds the exact result once, straight to fp16), which differs from the
+// reference's fp32 result rounded to fp16 whenever that result lies exactly
+// halfway between two fp16 values; the asm keeps the conversion on its own.
+// It equals the integer rounding (sign, rebiased exponent, 13 dropped
+// mantissa bits rounded half to even, subnormals below 2^-14, overflow from
+// 65520 on) for all 2^32 inputs, checked exhaustively on the device.
 __device__ __forceinline__ uint16_t f2h(float f) {
-    const uint32_t x = __float_as_uint(f);
-    const uint32_t sign = (x >> 16) & 0x8000u;
-    const uint32_t ax = x & 0x7FFFFFFFu;
-    if (ax >= 0x7F800000u) return (uint16_t)(sign | (ax > 0x7F800000u ? 0x7E00u : 0x7C00u));
-    if (ax >= 0x477FF000u) return (uint16_t)(sign | 0x7C00u);  // rounds past 65504
-    if (ax < 0x33000000u) return (uint16_t)sign;                // at most 2^-25: zero
-    uint32_t r, rem, half;
-    if (ax < 0x38800000u) {  // fp16 subnormal: keep the bits above 2^-24
-        const uint32_t shift = 126u - (ax >> 23);  // 14..24
-        const uint32_t m = (ax & 0x7FFFFFu) | 0x800000u;
-        r = m >> shift;
-        rem = m & ((1u << shift) - 1u);
-        half = 1u << (shift - 1u);
-    } else {                 // normal: rebias the exponent, drop 13 mantissa bits
-        r = (ax >> 13) - (112u << 10);
-        rem = ax & 0x1FFFu;
-        half = 0x1000u;
-    }
-    r += (rem > half || (rem == half && (r & 1u))) ? 1u : 0u;
-    return (uint16_t)(sign | r);
+    uint32_t h;
+    asm("v_cvt_f16_f32 %0, %1" : "=v"(h) : "v"(f));
+    return (uint16_t)h;
 }
 
 // s_waitcnt lgkmcnt(0) alone. A batch of 16 LDS reads issued behind another
