@@ -203,7 +203,7 @@ constexpr int ATT_KITEMS = ATT_CH * (ATT_HD / 8) / ATT_THREADS;  // 16-byte key 
 
 template <bool PAR>
 __global__ __launch_bounds__(ATT_THREADS) void attn_scores_kernel(AttnArgs a) {
-    __shared__ float qsh[3][ATT_HD];
+    __shared__ __align__(16) float qsh[3][ATT_HD];
     __shared__ uint16_t ksh[ATT_CH * ATT_KSTR];
     __shared__ __align__(16) uint16_t vnew[PAR ? ATT_HD : 1];
     __shared__ __align__(16) uint32_t vsh[PAR ? ATT_CH / 2 * ATT_HD : 1];  // [t/2][d]: (v_2r[d], v_2r+1[d])
@@ -341,17 +341,47 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_scores_kernel(AttnArgs a) {
     const int rows = min(ATT_CH, n - t0);
     float score = -INFINITY;
     if (lane < rows) {
+        // 8 lane chains over the 128 dims (chain l takes dims i + l), in
+        // batches of 32 dims: a batch's key words and query values (12 LDS
+        // reads, within what the lgkm counter tells apart) are issued before
+        // the previous batch's 32 FMAs, two register sets used in turn
         float cc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
         const uint16_t *kr2 = ksh + lane * ATT_KSTR;
+        const float4 *q4 = reinterpret_cast<const float4 *>(qsh[wid]);
+        u32x4 KA[4], KB[4];
+        float4 QA[8], QB[8];
+        auto ld = [&](u32x4 *K, float4 *Q, int i0) {
 #pragma unroll
-        for (int i = 0; i < ATT_HD; i += 8) {
-            const u32x4 kk = *reinterpret_cast<const u32x4 *>(kr2 + i);
-            const uint32_t kw[4] = {kk.x, kk.y, kk.z, kk.w};
+            for (int u = 0; u < 4; ++u) K[u] = *reinterpret_cast<const u32x4 *>(kr2 + i0 + 8 * u);
 #pragma unroll
-            for (int l = 0; l < 8; ++l) {
-                const uint16_t hb = (uint16_t)(kw[l >> 1] >> (16 * (l & 1)));
-                cc[l] = fmaf(qsh[wid][i + l], h2f(hb), cc[l]);
+            for (int u = 0; u < 8; ++u) Q[u] = q4[i0 / 4 + u];
+        };
+        auto run = [&](const u32x4 *K, const float4 *Q) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const uint32_t kw[4] = {K[u].x, K[u].y, K[u].z, K[u].w};
+                const float qv[8] = {Q[2 * u].x, Q[2 * u].y, Q[2 * u].z, Q[2 * u].w,
+                                     Q[2 * u + 1].x, Q[2 * u + 1].y, Q[2 * u + 1].z, Q[2 * u + 1].w};
+#pragma unroll
+                for (int l = 0; l < 8; ++l) {
+                    const uint16_t hb = (uint16_t)(kw[l >> 1] >> (16 * (l & 1)));
+                    cc[l] = fmaf(qv[l], h2f(hb), cc[l]);
+                }
             }
+        };
+        ld(KA, QA, 0);
+#pragma unroll
+        for (int b = 0; b < 4; b += 2) {
+            lgkm_wait0();
+            __builtin_amdgcn_sched_barrier(0);
+            ld(KB, QB, 32 * (b + 1));
+            run(KA, QA);
+            __builtin_amdgcn_sched_barrier(0);
+            lgkm_wait0();
+            __builtin_amdgcn_sched_barrier(0);
+            if (b + 2 < 4) ld(KA, QA, 32 * (b + 2));
+            run(KB, QB);
+            __builtin_amdgcn_sched_barrier(0);
         }
         float dot;
         if (t >= (pos & ~7)) {  // text_layer.cpp:626-633: lanes folded left to right
