@@ -408,11 +408,20 @@ __global__ __launch_bounds__(256, BPC) void gemm_mf_kernel(GemmMfArgs a) {
                 asv[4 * q4 + 2] = v.z;
                 asv[4 * q4 + 3] = v.w;
             }
+            // The single-m-tile variant (M <= 32) skips the accumulator
+            // quads whose rows (8 (e / 4) + e % 4, and 4 more) are all past M:
+            // their outputs are never stored.
+            int nq = 4;
+            if constexpr (MTB == 1) nq = min(4, (M - 32 * mt0 + 7) >> 3);  // uniform
 #pragma unroll
-            for (int j = 0; j < TN; ++j)
+            for (int q = 0; q < 4; ++q) {
+                if (q >= nq) break;
 #pragma unroll
-                for (int e = 0; e < 16; ++e)
-                    out[i][j][e] = fmaf(acc[i][j][e] * asv[e], ws_g[j], out[i][j][e]);
+                for (int j = 0; j < TN; ++j)
+#pragma unroll
+                    for (int e = 4 * q; e < 4 * q + 4; ++e)
+                        out[i][j][e] = fmaf(acc[i][j][e] * asv[e], ws_g[j], out[i][j][e]);
+            }
         }
     };
     // group g = g0 + j (ring slot sl = j % D): MFMAs, reload slot sl with
