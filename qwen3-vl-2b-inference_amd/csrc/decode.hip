@@ -629,13 +629,18 @@ __global__ __launch_bounds__(PV_THREADS) void attn_softmax_pv_kernel(AttnArgs a)
     // chunk maxima: wave hh < kvm, lane c (one pass covers 4096 positions)
     const int wh = min(wid, kvm - 1);
     const float cm = a.cmax[(kvh * kvm + wh) * a.max_chunks + min(lane, a.max_chunks - 1)];
-    // scores: thread tid holds positions 4*(tid + PV_THREADS*k) + 0..3
+    // scores: for head hh, thread tid holds positions 4*(ti + PV_THREADS*k)
+    // + 0..3 with ti = tid on even heads and PV_THREADS-1-tid on odd ones,
+    // so the float4s past a multiple of PV_THREADS fall to wave 0 on one
+    // head and to the last wave on the next, and no wave computes every
+    // head's tail
     float4 sreg[3][PV_SREG];
 #pragma unroll
     for (int hh = 0; hh < 3; ++hh) {
         const float4 *sc = reinterpret_cast<const float4 *>(a.scores + (size_t)(kvh * kvm + min(hh, kvm - 1)) * S);
+        const int ti = (hh & 1) ? PV_THREADS - 1 - tid : tid;
 #pragma unroll
-        for (int k = 0; k < PV_SREG; ++k) sreg[hh][k] = sc[min(tid + PV_THREADS * k, S / 4 - 1)];
+        for (int k = 0; k < PV_SREG; ++k) sreg[hh][k] = sc[min(ti + PV_THREADS * k, S / 4 - 1)];
     }
     // V chunk 0: every thread loads its share at entry (thread tid: vsg =
     // tid & 1, vb = tid >> 1, quads vb and vb + 128) and widens it into LDS
@@ -644,7 +649,8 @@ __global__ __launch_bounds__(PV_THREADS) void attn_softmax_pv_kernel(AttnArgs a)
     // chain runs on the previous one, so the chain wave issues no loads.
     u32x4 vr0[4 * PV_Q0], vrn[4 * PV_QN];
     const int vsg = tid & 1;
-    const bool stager = __builtin_amdgcn_readfirstlane(wid) >= 2;  // wave-uniform
+    const int wu = __builtin_amdgcn_readfirstlane(wid);  // wave-uniform
+    const bool stager = wu >= 2;
     __builtin_amdgcn_sched_barrier(0);
     pv_load<PV_Q0, PV_THREADS / 2>(vr0, vc, 0, S, vsg, tid >> 1);
     __builtin_amdgcn_sched_barrier(0);
@@ -657,7 +663,6 @@ __global__ __launch_bounds__(PV_THREADS) void attn_softmax_pv_kernel(AttnArgs a)
     const int n = pos + 1;
     const int nb = n & ~7;
     const int nch = (n + ATT_CH - 1) / ATT_CH;
-    const int kreg = min(PV_SREG, (n + 4 * PV_THREADS - 1) / (4 * PV_THREADS));  // uniform
     auto chunk_lim = [&](int t0) { return (min(PV_TC, n - t0) + 63) & ~63; };
 
     // ---- M per head from the chunk maxima (beyond one pass: loop)
@@ -701,9 +706,13 @@ __global__ __launch_bounds__(PV_THREADS) void attn_softmax_pv_kernel(AttnArgs a)
         // per lane: adding +0 to a sum of non-negative terms is exact
         const int zend = (nb + 255) & ~255;
         for (int t = nb + tid; t < zend; t += PV_THREADS) eth[(t & 7) * ets + (t >> 3)] = 0.0f;
+        // a wave skips a k with no position below n (uniform: its lowest
+        // float4 index is 64*wid + PV_THREADS*k, mirrored on odd heads)
+        const int ti = (hh & 1) ? PV_THREADS - 1 - tid : tid;
+        const int wlo = (hh & 1) ? PV_THREADS - 64 * (wu + 1) : 64 * wu;
 #pragma unroll
         for (int k = 0; k < PV_SREG; ++k)
-            if (k < kreg) put4(4 * (tid + PV_THREADS * k), sreg[hh][k]);
+            if (4 * (wlo + PV_THREADS * k) < n) put4(4 * (ti + PV_THREADS * k), sreg[hh][k]);
         const float4 *sc = reinterpret_cast<const float4 *>(a.scores + (size_t)(kvh * kvm + hh) * S);
         for (int i = tid + PV_THREADS * PV_SREG; 4 * i < n; i += PV_THREADS) put4(4 * i, sc[i]);
     }
