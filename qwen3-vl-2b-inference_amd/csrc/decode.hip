@@ -356,7 +356,16 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_scores_kernel(AttnArgs a) {
 #pragma unroll
             for (int u = 0; u < 8; ++u) Q[u] = q4[i0 / 4 + u];
         };
+        // the chains pass through an empty asm before and after each batch:
+        // otherwise instruction selection, which keeps plain arithmetic in
+        // no order against the waits, gathers the FMAs of the later batches
+        // behind the last reads and every batch's read latency is waited out
+        auto pin = [&]() {
+            asm volatile("" : "+v"(cc[0]), "+v"(cc[1]), "+v"(cc[2]), "+v"(cc[3]),
+                              "+v"(cc[4]), "+v"(cc[5]), "+v"(cc[6]), "+v"(cc[7]));
+        };
         auto run = [&](const u32x4 *K, const float4 *Q) {
+            pin();
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
                 const uint32_t kw[4] = {K[u].x, K[u].y, K[u].z, K[u].w};
@@ -368,6 +377,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_scores_kernel(AttnArgs a) {
                     cc[l] = fmaf(qv[l], h2f(hb), cc[l]);
                 }
             }
+            pin();
         };
         ld(KA, QA, 0);
 #pragma unroll

@@ -74,11 +74,12 @@ def test_decode_edge_positions(dev, orc, pos):
     Stepper(dev, orc, dims, seed=30 + pos, ctx=pos, token=pos % 4096).step()
 
 
-@pytest.mark.parametrize("pos", [1023, 1024, 1100])
+@pytest.mark.parametrize("pos", [511, 512, 1023, 1024, 1100, 1535, 1536])
 def test_decode_context_past_one_value_chunk(dev, orc, pos):
-    """Contexts of 1024, 1025 and 1101 positions: the value-weighted sum
-    stages V through LDS in chunks of 1024 positions."""
-    dims = dict(SMALL, layers=1, max_seq=1280)
+    """Contexts of 512 to 1537 positions, on either side of 512, 1024 and
+    1536: the value-weighted sum stages V through LDS in chunks of 1024
+    positions."""
+    dims = dict(SMALL, layers=1, max_seq=1600)
     Stepper(dev, orc, dims, seed=40, ctx=pos, token=11).step()
 
 
