@@ -112,6 +112,34 @@ def test_decode_position_out_of_range(dev):
     np.testing.assert_array_equal(vd.cpu().numpy(), v16.view(np.int16))
 
 
+@pytest.mark.parametrize("gs,token", [(64, -1), (64, 4096), (32, 4096)])
+def test_decode_token_out_of_range(dev, gs, token):
+    """A token outside [0, vocab) reads no table row: its embedding is a NaN
+    row, so the logits are NaN, the greedy id is 0 (NaN never wins), the
+    cache rows at pos hold NaN and every other row is untouched (group 64,
+    the decode step's, and 32)."""
+    torch, qm = dev
+    dims = dict(SMALL, layers=1, gs=gs)
+    m = make_text_model(75, dims)
+    k16, v16 = make_kv_cache(76, dims, 100)
+    model = qm.DeviceTextModel(dims, m)
+    kd = torch.from_numpy(k16.view(np.int16).copy()).cuda()
+    vd = torch.from_numpy(v16.view(np.int16).copy()).cuda()
+    tok = torch.tensor([token], dtype=torch.int32, device="cuda")
+    pos = torch.tensor([100], dtype=torch.int32, device="cuda")
+    logits = torch.zeros(dims["vocab"], dtype=torch.float32, device="cuda")
+    qm.decode_step(model, kd, vd, tok, pos, logits, qm.alloc_decode_workspace(model))
+    torch.cuda.synchronize()
+    assert torch.isnan(logits).all()
+    assert int(tok.item()) == 0 and int(pos.item()) == 101
+    for got, ref in ((kd, k16), (vd, v16)):
+        g = got.cpu().numpy().view(np.float16)
+        assert np.isnan(g[:, :, 100]).all()
+        keep = np.ones(g.shape[2], bool)
+        keep[100] = False
+        np.testing.assert_array_equal(g[:, :, keep].view(np.uint16), ref[:, :, keep].view(np.uint16))
+
+
 @pytest.mark.parametrize("gs", [32, 128])
 def test_decode_other_group_sizes(dev, orc, gs):
     """The exporter's other group sizes (export_qwen_bin.py:371): every GEMV,
