@@ -105,8 +105,14 @@ __host__ __device__ constexpr int norm_row_words(int K, bool seg) {
 // once for all of them, with the staging spread over the whole block, so a CU
 // no longer repeats that work for every resident block. (Decode shapes:
 // K = 2048, group 64, one activation row.)
+// The segments' weight and scale pointers and first two row counts come
+// first, as plain arguments, so that they arrive preloaded in scalar
+// registers (kernel-argument preloading takes leading non-aggregate
+// arguments only) and the first weight loads wait for no argument fetch.
 template <int GS, int MR, bool LANES, int R, int KC, int MD, int P = 1>
-__global__ __launch_bounds__(GEMV_MAX_THREADS) void gemv_kernel(GemvArgs a, int ntiles) {
+__global__ __launch_bounds__(GEMV_MAX_THREADS) void gemv_kernel(
+    const int8_t *W0, const int8_t *W1, const int8_t *W2, const float *S0, const float *S1,
+    const float *S2, int N0, int N1, GemvArgs a, int ntiles) {
     static_assert(P == 1 || (P == 4 && KC == 2048 && GS == 64 && MR == 1 && LANES),
                   "shared-prologue blocks serve the decode shapes only");
     constexpr int T = GS / 16;
@@ -133,11 +139,11 @@ __global__ __launch_bounds__(GEMV_MAX_THREADS) void gemv_kernel(GemvArgs a, int 
     const bool swg = mode == GEMV_SWIGLU;
 
     SegRegs sr;
-    sr.W0 = a.seg[0].W; sr.W1 = a.seg[1].W; sr.W2 = a.seg[2].W;
-    sr.S0 = a.seg[0].S; sr.S1 = a.seg[1].S; sr.S2 = a.seg[2].S;
+    sr.W0 = W0; sr.W1 = W1; sr.W2 = W2;
+    sr.S0 = S0; sr.S1 = S1; sr.S2 = S2;
     sr.Y0 = a.seg[0].Y; sr.Y1 = a.seg[1].Y; sr.Y2 = a.seg[2].Y;
     sr.G0 = a.seg[0].G; sr.G1 = a.seg[1].G; sr.G2 = a.seg[2].G;
-    sr.N0 = a.seg[0].N; sr.N1 = a.seg[1].N; sr.N2 = a.seg[2].N;
+    sr.N0 = N0; sr.N1 = N1; sr.N2 = a.seg[2].N;
     const float *Ap = a.A;
     const int8_t *norm_w = a.norm_w;
     const float *norm_s = a.norm_s;
@@ -1001,7 +1007,9 @@ static hipError_t launch_gemv_t(const GemvArgs &a, int *grid_out, hipStream_t st
     if (grid > (ntiles + P - 1) / P) grid = (ntiles + P - 1) / P;
     if (grid < 1) grid = 1;
     if (grid_out) *grid_out = grid;
-    gemv_kernel<GS, MR, LANES, R, KC, MD, P><<<grid, P * nthr, lds, st>>>(a, ntiles);
+    gemv_kernel<GS, MR, LANES, R, KC, MD, P><<<grid, P * nthr, lds, st>>>(
+        a.seg[0].W, a.seg[1].W, a.seg[2].W, a.seg[0].S, a.seg[1].S, a.seg[2].S, a.seg[0].N,
+        a.seg[1].N, a, ntiles);
     return hipGetLastError();
 }
 
