@@ -201,8 +201,24 @@ constexpr int ATT_KSTR = ATT_HD + 8;  // halves per LDS key row (272 B: bank-spr
 constexpr int ATT_THREADS = 256;
 constexpr int ATT_KITEMS = ATT_CH * (ATT_HD / 8) / ATT_THREADS;  // 16-byte key pieces per thread
 
+// The attention kernels take what their entry loads need as leading plain
+// arguments (the position pointer first), which the dispatcher preloads into
+// scalar registers: the position's load then waits for no argument fetch.
+// The rest is read from the AttnArgs copy after them.
 template <bool PAR>
-__global__ __launch_bounds__(ATT_THREADS) void attn_scores_kernel(AttnArgs a) {
+__global__ __launch_bounds__(ATT_THREADS) void attn_scores_kernel(
+    const int32_t *pos_p, uint16_t *k_cache_p, const float *q_p, const float *k_p,
+    const int8_t *qnorm_w_p, int layer_p, int heads_p, int kv_heads_p, int max_seq_p, AttnArgs args) {
+    AttnArgs a = args;
+    a.pos = pos_p;
+    a.k_cache = k_cache_p;
+    a.q = q_p;
+    a.k = k_p;
+    a.qnorm_w = qnorm_w_p;
+    a.layer = layer_p;
+    a.heads = heads_p;
+    a.kv_heads = kv_heads_p;
+    a.max_seq = max_seq_p;
     __shared__ __align__(16) float qsh[3][ATT_HD];
     __shared__ uint16_t ksh[ATT_CH * ATT_KSTR];
     __shared__ __align__(16) uint16_t vnew[PAR ? ATT_HD : 1];
@@ -614,7 +630,19 @@ __host__ __device__ __forceinline__ int pv_et_stride(int max_seq) {
     return (max_seq / 8 + 31) / 32 * 32 + 4;
 }
 
-__global__ __launch_bounds__(PV_THREADS) void attn_softmax_pv_kernel(AttnArgs a) {
+__global__ __launch_bounds__(PV_THREADS) void attn_softmax_pv_kernel(
+    const int32_t *pos_p, const float *scores_p, const float *cmax_p, const uint16_t *v_cache_p,
+    int layer_p, int heads_p, int kv_heads_p, int max_seq_p, int max_chunks_p, AttnArgs args) {
+    AttnArgs a = args;
+    a.pos = pos_p;
+    a.scores = const_cast<float *>(scores_p);
+    a.cmax = const_cast<float *>(cmax_p);
+    a.v_cache = const_cast<uint16_t *>(v_cache_p);
+    a.layer = layer_p;
+    a.heads = heads_p;
+    a.kv_heads = kv_heads_p;
+    a.max_seq = max_seq_p;
+    a.max_chunks = max_chunks_p;
     extern __shared__ __align__(16) float smem[];
     const int kvm = a.heads / a.kv_heads;
     const int S = a.max_seq, ets = pv_et_stride(S);
@@ -863,13 +891,15 @@ hipError_t launch_attention(const AttnArgs &a, hipStream_t st) {
     if (lds > kAttnMaxLds) return hipErrorInvalidValue;
     if (a.order == 1) {  // chunked order
         if (!a.part_o || !a.part_ml || a.max_chunks > ATT_MAX_CHUNKS) return hipErrorInvalidValue;
-        attn_scores_kernel<true><<<dim3(a.kv_heads, a.max_chunks), ATT_THREADS, 0, st>>>(a);
+        attn_scores_kernel<true><<<dim3(a.kv_heads, a.max_chunks), ATT_THREADS, 0, st>>>(
+            a.pos, a.k_cache, a.q, a.k, a.qnorm_w, a.layer, a.heads, a.kv_heads, a.max_seq, a);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
         attn_combine_kernel<<<a.heads, ATT_HD, 0, st>>>(a);
         return hipGetLastError();
     }
-    attn_scores_kernel<false><<<dim3(a.kv_heads, a.max_chunks), ATT_THREADS, 0, st>>>(a);
+    attn_scores_kernel<false><<<dim3(a.kv_heads, a.max_chunks), ATT_THREADS, 0, st>>>(
+        a.pos, a.k_cache, a.q, a.k, a.qnorm_w, a.layer, a.heads, a.kv_heads, a.max_seq, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     static int lds_set = 0;  // raise the dynamic LDS limit once per process
@@ -879,7 +909,8 @@ hipError_t launch_attention(const AttnArgs &a, hipStream_t st) {
         if (e != hipSuccess) return e;
         lds_set = 1;
     }
-    attn_softmax_pv_kernel<<<dim3(a.kv_heads, ATT_HD / PV_D), PV_THREADS, lds, st>>>(a);
+    attn_softmax_pv_kernel<<<dim3(a.kv_heads, ATT_HD / PV_D), PV_THREADS, lds, st>>>(
+        a.pos, a.scores, a.cmax, a.v_cache, a.layer, a.heads, a.kv_heads, a.max_seq, a.max_chunks, a);
     return hipGetLastError();
 }
 
