@@ -149,7 +149,22 @@ __device__ __forceinline__ int bslot(int s, int l) {
 // power of two, at most kWsTile; K must be a multiple of 64 kWsTile).
 constexpr int kWsTile = 8;
 template <int TM, int TN, bool SWIGLU, int D, int BPC, int WM = 2, bool AL = true, int SG = kWsTile>
-__global__ __launch_bounds__(256, BPC) void gemm_mf_kernel(GemmMfArgs a) {
+// What the entry loads need comes first, as plain arguments that the
+// dispatcher preloads into scalar registers (the up scales and the rest are
+// read from the GemmMfArgs copy).
+__global__ __launch_bounds__(256, BPC) void gemm_mf_kernel(
+    const _Float16 *Af_p, const float *asf_p, const int8_t *W0_p, const float *S0_p, int Mt_p,
+    int N_p, int K_p, int M_p, const int8_t *W1_p, GemmMfArgs args) {
+    GemmMfArgs a = args;
+    a.Af = Af_p;
+    a.asf = asf_p;
+    a.W0 = W0_p;
+    a.S0 = S0_p;
+    a.Mt = Mt_p;
+    a.N = N_p;
+    a.K = K_p;
+    a.M = M_p;
+    a.W1 = W1_p;
     constexpr int WN = 4 / WM;              // waves along N
     constexpr int MTB = WM * TM;            // m-tiles of the block
     constexpr int BN = 32 * WN * TN;        // weight rows of the block
@@ -557,7 +572,8 @@ static hipError_t launch_mf(const GemmMfArgs &a, hipStream_t st) {
     const int tiles = ((a.N + ncols - 1) / ncols) * ((a.Mt + MTB - 1) / MTB);
     const int grid = 8 * ((tiles + 7) / 8);  // see the tile order in the kernel
     const size_t lds = 2 * (BN / 32) * 4 * 64 * 16 + (AL ? 2 * MTB * 4096 : 0) + 2 * 32 * MTB * 4 + 2 * SG * BN * 4;
-    gemm_mf_kernel<TM, TN, SWIGLU, D, BPC, WM, AL, SG><<<grid, 256, lds, st>>>(a);
+    gemm_mf_kernel<TM, TN, SWIGLU, D, BPC, WM, AL, SG><<<grid, 256, lds, st>>>(
+        a.Af, a.asf, a.W0, a.S0, a.Mt, a.N, a.K, a.M, a.W1, a);
     return hipGetLastError();
 }
 
