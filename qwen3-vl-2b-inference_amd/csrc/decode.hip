@@ -477,7 +477,15 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_scores_kernel(
 // values it feeds are needed: the (m_c, l_c) pairs of all chunks go to LDS
 // in one pass (one chunk per thread), the o_c[d] in batches of 16.
 constexpr int ATT_MAX_CHUNKS = 256;  // max_seq <= 16384
-__global__ __launch_bounds__(ATT_HD) void attn_combine_kernel(AttnArgs a) {
+__global__ __launch_bounds__(ATT_HD) void attn_combine_kernel(
+    const int32_t *pos_p, const float *part_ml_p, const float *part_o_p, int max_chunks_p, int max_seq_p,
+    AttnArgs args) {
+    AttnArgs a = args;  // leading arguments preloaded, as in the kernels above
+    a.pos = pos_p;
+    a.part_ml = const_cast<float *>(part_ml_p);
+    a.part_o = const_cast<float *>(part_o_p);
+    a.max_chunks = max_chunks_p;
+    a.max_seq = max_seq_p;
     __shared__ float wsh[ATT_MAX_CHUNKS], lsh[ATT_MAX_CHUNKS], msh[ATT_MAX_CHUNKS];
     __shared__ float mred[2];
     const int h = blockIdx.x, d = threadIdx.x, lane = d & 63;
@@ -895,7 +903,8 @@ hipError_t launch_attention(const AttnArgs &a, hipStream_t st) {
             a.pos, a.k_cache, a.q, a.k, a.qnorm_w, a.layer, a.heads, a.kv_heads, a.max_seq, a);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
-        attn_combine_kernel<<<a.heads, ATT_HD, 0, st>>>(a);
+        attn_combine_kernel<<<a.heads, ATT_HD, 0, st>>>(a.pos, a.part_ml, a.part_o, a.max_chunks,
+                                                         a.max_seq, a);
         return hipGetLastError();
     }
     attn_scores_kernel<false><<<dim3(a.kv_heads, a.max_chunks), ATT_THREADS, 0, st>>>(
