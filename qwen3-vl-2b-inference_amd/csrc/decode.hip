@@ -515,9 +515,9 @@ __global__ __launch_bounds__(ATT_HD) void attn_combine_kernel(
         lsh[c] = v.y;
         m = fmaxf(m, v.x);
     }
-    // M: the max of the m_c (a max is the same in any order)
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    // M: the max of the m_c (a max is the same in any order: DPP moves
+    // instead of wave shuffles, which are LDS round trips)
+    m = wave_max(m);
     if (lane == 0) mred[d >> 6] = m;
     __syncthreads();
     const float M = fmaxf(mred[0], mred[1]);
@@ -716,8 +716,7 @@ __global__ __launch_bounds__(PV_THREADS) void attn_softmax_pv_kernel(
         const float *cmh = a.cmax + (kvh * kvm + wid) * a.max_chunks;
         float m = lane < nch ? cm : -INFINITY;  // loaded for head wh == wid
         for (int c = lane + 64; c < nch; c += 64) m = fmaxf(m, cmh[c]);
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+        m = wave_max(m);  // (any order: DPP moves, no LDS round trips)
         if (lane == 0) hmax[wid] = m;
     }
     lds_barrier();
