@@ -356,10 +356,11 @@ def _event_time(fn, steps, warmup):
     return e0.elapsed_time(e1) / steps
 
 
-def _graph_time(fns, reps=5, trials=5):
+def _graph_time(fns, reps=5, trials=5, region=None):
     """ms per call of the calls in fns, captured once into a HIP graph and
     replayed (median of `trials` timings of `reps` replays): the kernels'
-    own time, without the per-call host overhead of eager launches."""
+    own time, without the per-call host overhead of eager launches. With a
+    region tag the timed replays sit between that region's trace markers."""
     import torch
     for fn in fns:  # eager pass: first use
         fn()
@@ -370,6 +371,8 @@ def _graph_time(fns, reps=5, trials=5):
             fn()
     g.replay()
     torch.cuda.synchronize()
+    if region:
+        region_mark(region)
     st = torch.cuda.current_stream()
     out = []
     for _ in range(trials):
@@ -380,7 +383,26 @@ def _graph_time(fns, reps=5, trials=5):
         e1.record(st)
         torch.cuda.synchronize()
         out.append(e0.elapsed_time(e1) / (reps * len(fns)))
+    if region:
+        region_mark(region)
     return sorted(out)[len(out) // 2]
+
+
+# Kernel-trace regions: each timed section is bracketed by two swiglu_kernel
+# launches (no bench leg launches that kernel otherwise) of REGION_BLOCKS[tag]
+# blocks, so `--trace-summary` attributes the profiler's own durations to the
+# section that produced them.
+REGION_BLOCKS = {"cfg1_gemv": 1, "cfg0": 2, "cfg2": 3, "cfg3_m1": 4, "cfg3_m8": 5, "cfg4": 6}
+
+
+def region_mark(tag):
+    import torch
+    import q3vl_int8 as q
+    n = 256 * (REGION_BLOCKS[tag] - 1) + 1
+    marker = torch.zeros(n, dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    q.swiglu(marker, marker)
+    torch.cuda.synchronize()
 
 
 def gen_weights(N, K, copies, seed, device="cuda"):
@@ -554,9 +576,7 @@ def decode_gemv_roofline(model, dims):
         g.replay()
         torch.cuda.synchronize()
         graphs[name] = g
-    marker = torch.zeros(1, dtype=torch.float32, device="cuda")
-    q.swiglu(marker, marker)  # region start (kernel-trace marker)
-    torch.cuda.synchronize()
+    region_mark("cfg1_gemv")  # region start (kernel-trace marker)
     st = torch.cuda.current_stream()
     res = {}
     for name, (fns, nbytes) in kinds.items():
@@ -573,8 +593,7 @@ def decode_gemv_roofline(model, dims):
         us = sorted(trials)[len(trials) // 2]
         res[name] = dict(us=us, bytes=nbytes, GBs=nbytes / (us * 1e-6) / 1e9,
                          launches_timed=25 * len(fns))
-    q.swiglu(marker, marker)  # region end
-    torch.cuda.synchronize()
+    region_mark("cfg1_gemv")  # region end
     step_us = sum(res[k]["us"] * n for k, n in per_step.items())
     step_bytes = sum(res[k]["bytes"] * n for k, n in per_step.items())
     launches = sum(per_step.values())
@@ -599,7 +618,7 @@ def bench_cfg0(args):
     eager_ms = _event_time(call, max(args.steps, 200), 20)
     # One graph of the n launches (one per weight copy), replayed: a 6 us
     # kernel is shorter than a Python call, so eager calls would time the host
-    ms = _graph_time([lambda i=i: call(i) for i in range(n)])
+    ms = _graph_time([lambda i=i: call(i) for i in range(n)], region="cfg0")
     algo = wbytes(N, K) + K * 4 + N * 4
     gbs = algo / (ms * 1e-3) / 1e9
     return dict(name="cfg0_up_proj_gemv", metric="GB/s", value=gbs, ms=ms, eager_ms=eager_ms,
@@ -620,15 +639,18 @@ def bench_cfg2(args):
     D = torch.empty((M, K), dtype=torch.float32, device="cuda")
     ws = q.alloc_workspace(M, I, max(K, I), GS)
 
-    def step(i):
+    def step():
         q.linear_i8_swiglu(A, Wg[0], Sg[0], Wu[0], Su[0], GS, out=H, workspace=ws)
         q.linear_i8(H, Wd[0], Sd[0], GS, out=D, workspace=ws)
 
-    ms = _event_time(step, max(args.steps // 2, 50), 5)
+    # one HIP graph of the step (two quantizers and two GEMMs), replayed: the
+    # kernels back to back, without the host time of eager Python calls
+    ms = _graph_time([step], reps=10, region="cfg2")
     ops = cfg2_ops(M, K, I)
     tops = ops / (ms * 1e-3) / 1e12
     return dict(name="cfg2_prefill_gemm", metric="TOPS", value=tops, ms=ms, algo_ops=ops,
                 frac=tops / FP16_PEAK_TFLOPS, frac_of_int8_peak=tops / INT8_PEAK_TOPS,
+                timing="HIP-graph replay of the step (quantizers and GEMMs)",
                 kernel="quantize_frag_kernel + gemm_mf_kernel: gate|up with the SwiGLU "
                        "epilogue, then down")
 
@@ -644,8 +666,13 @@ def bench_cfg3(args, M):
     ws = q.alloc_workspace(M, V, K, GS)
     # eager: each call keeps the device busy for ~60-190 us, longer than the
     # host needs to issue the next, so no host time is inside the figure
-    ms = _event_time(lambda i: q.lm_head_argmax(x, Ws[i % n], Ss[i % n], GS, ids=ids, workspace=ws),
-                     max(args.steps // 2, 50), 6)
+    call = lambda i: q.lm_head_argmax(x, Ws[i % n], Ss[i % n], GS, ids=ids, workspace=ws)
+    for i in range(6):  # warm-up
+        call(i)
+    torch.cuda.synchronize()
+    region_mark(f"cfg3_m{M}")
+    ms = _event_time(call, max(args.steps // 2, 50), 0)
+    region_mark(f"cfg3_m{M}")
     algo = wbytes(V, K) + M * K * 4 + M * 4
     gbs = algo / (ms * 1e-3) / 1e9
     return dict(name=f"cfg3_lm_head_argmax_m{M}", metric="GB/s", value=gbs, ms=ms, algo_bytes=algo,
@@ -669,7 +696,7 @@ def bench_cfg4(args):
     outM = {N: torch.empty((T // 4, N), dtype=torch.float32, device="cuda") for N, _ in MERGER_SHAPES}
     ws = q.alloc_workspace(T, 3 * D, F, GS)
 
-    def step(i):
+    def step():
         for b in range(B):
             for j, (N, K) in enumerate(VIS_SHAPES):
                 (W,), (S,) = Wb[b][j]
@@ -678,12 +705,14 @@ def bench_cfg4(args):
             (W,), (S,) = Wm[j]
             q.linear_i8(xM, W, S, GS, out=outM[N], workspace=ws)
 
-    ms = _event_time(step, max(args.steps // 20, 10), 2)
+    # one HIP graph of the pass (98 quantizers and 98 GEMMs), replayed
+    ms = _graph_time([step], reps=3, region="cfg4")
     ops = cfg4_ops()
     tops = ops / (ms * 1e-3) / 1e12
     return dict(name="cfg4_vision_linears", metric="TOPS", value=tops, ms=ms, algo_ops=ops,
                 frac=tops / FP16_PEAK_TFLOPS, frac_of_int8_peak=tops / INT8_PEAK_TOPS,
                 gemms=B * len(VIS_SHAPES) + len(MERGER_SHAPES),
+                timing="HIP-graph replay of the pass (quantizers and GEMMs)",
                 kernel="quantize_frag_kernel + gemm_mf_kernel (K a multiple of 512: every "
                        "vision and merger linear)")
 
@@ -820,7 +849,15 @@ def trace_summary(path):
             rows.append((t0, t1, name, grid))
     rows.sort()
     marks = [i for i, r in enumerate(rows) if "swiglu_kernel" in r[2]]
-    region = rows[marks[0] + 1:marks[1]] if len(marks) >= 2 else []
+    tag_of = {v: k for k, v in REGION_BLOCKS.items()}
+    regions = {}
+    for a, b in zip(marks[0::2], marks[1::2]):
+        blocks = rows[a][3].split("x")[0]
+        try:
+            tag = tag_of.get(int(blocks) // 256, f"grid {blocks}")
+        except ValueError:
+            tag = f"grid {blocks}"
+        regions.setdefault(tag, []).extend(rows[a + 1:b])
 
     def agg(rs):
         d = {}
@@ -831,8 +868,12 @@ def trace_summary(path):
         return {k: dict(calls=c, avg_us=round(tot / c, 3), total_us=round(tot, 1))
                 for k, (c, tot) in sorted(d.items(), key=lambda kv: -kv[1][1])}
 
-    return dict(trace=path, dispatches=len(rows), markers=len(marks),
-                roofline_region=agg(region), whole_run=agg(rows))
+    out = dict(trace=path, dispatches=len(rows), markers=len(marks))
+    for tag, rs in regions.items():
+        out[f"region {tag}"] = agg(rs)
+        out[f"region {tag} total_us"] = round(sum((t1 - t0) / 1000.0 for t0, t1, _, _ in rs), 1)
+    out["whole_run"] = agg(rows)
+    return out
 
 
 # ===================================================================== main

@@ -61,51 +61,74 @@ typedef float float16_t __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // ---------------------------------------------------- fragment-order quantizer
-// The reference quantizer (cpu_f32a_i8f32sb_f32c_avx2.cpp:135-177), as
-// quantize_rows_kernel computes it (16 lanes per group: lane i runs the FMA
-// chain over x[16t + i], then the fixed tree), writing q as fp16 in the
-// fragment order above and a_s in its fragment order. Rows M .. 32*Mt-1 are
-// written as zeros. A 256-thread block takes 8 consecutive rows of an m-tile
-// and 2 groups (16 lanes per row and group): a 128-byte line of the fragment
-// order holds 16 bytes of each of 8 consecutive rows, so every line is
-// written whole by one block (rows of a line spread over blocks on several
-// XCDs would leave partial lines in several L2s).
+// The reference quantizer (cpu_f32a_i8f32sb_f32c_avx2.cpp:135-177) writing q
+// as fp16 in the fragment order above and a_s in its fragment order; rows
+// M .. 32*Mt-1 are written as zeros. 16 lanes per (row, group): lane u loads
+// the float4 of elements 4u .. 4u+3 (one coalesced 256-byte row piece per 16
+// lanes). The group's sum of squares runs in the reference order in
+// registers: chain 4(u & 3) + k takes elements 16t + 4(u & 3) + k, t = 0..3,
+// whose step t lives in lane 4t + (u & 3), so each of four rounds extends the
+// chain value of lane u - 4 (row_shr:4; 0 into lanes 0..3) and lanes 12..15
+// end with the 16 chains; V[i] = P0[i] + P1[i] (lanes 12, 13 take lanes 14,
+// 15: row_shl:2), lane 12 takes lane 13's half (row_shl:1), runs the fixed
+// tree, and the row takes lane 12's sum (row_newbcast:12). Each lane then
+// quantizes its 4 values and stores them as 8 bytes of fp16: elements 4u ..
+// 4u+3 are halves 4(u & 1) .. of slice (u & 7) / 2 in lane half u / 8. A
+// block takes 8 rows x 2 groups: a 128-byte line of the fragment order holds
+// 16 bytes of each of 8 consecutive rows, so every line is written whole by
+// one block (rows of a line spread over blocks on several XCDs would leave
+// partial lines in several L2s).
 __global__ __launch_bounds__(256) void quantize_frag_kernel(const float *__restrict__ A,
                                                             _Float16 *__restrict__ qf,
                                                             float *__restrict__ asf, int M, int K) {
     const int Kg = K / 64;
-    const int lane16 = threadIdx.x & 15;
-    const int pair = threadIdx.x >> 4;  // row pair & 7, group pair >> 3 of the block
-    const int g = blockIdx.x * 2 + (pair >> 3);
-    const int m = blockIdx.y * 8 + (pair & 7);
-    if (g >= Kg) return;  // whole 16-lane groups leave together
+    const int u = threadIdx.x & 15;
+    const int pair = threadIdx.x >> 4;  // row (pair & 3) + 4 (pair >> 3), group pair >> 2 & 1
+    const int g = blockIdx.x * 2 + ((pair >> 2) & 1);
+    const int m = blockIdx.y * 8 + (pair & 3) + 4 * (pair >> 3);
+    if (g >= Kg) return;  // whole 16-lane rows leave together
     const bool real = m < M;
-    const float *x = A + (size_t)(real ? m : 0) * K + (size_t)g * 64;
-    float v[4];
-    float p = 0.0f;
+    float4 xv = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (real) xv = reinterpret_cast<const float4 *>(A + (size_t)m * K + (size_t)g * 64)[u];
+#define Q3VL_DPPF(v, ctrl) \
+    __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), ctrl, 0xF, 0xF, false))
+    float c0 = fmaf(xv.x, xv.x, 0.0f), c1 = fmaf(xv.y, xv.y, 0.0f);
+    float c2 = fmaf(xv.z, xv.z, 0.0f), c3 = fmaf(xv.w, xv.w, 0.0f);
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-        v[t] = x[16 * t + lane16];
-        p = fmaf(v[t], v[t], p);
+    for (int t = 1; t < 4; ++t) {
+        c0 = fmaf(xv.x, xv.x, Q3VL_DPPF(c0, 0x114));
+        c1 = fmaf(xv.y, xv.y, Q3VL_DPPF(c1, 0x114));
+        c2 = fmaf(xv.z, xv.z, Q3VL_DPPF(c2, 0x114));
+        c3 = fmaf(xv.w, xv.w, Q3VL_DPPF(c3, 0x114));
     }
-    p = p + __shfl_xor(p, 8, 16);
-    p = p + __shfl_xor(p, 4, 16);
-    p = p + __shfl_xor(p, 1, 16);
-    p = p + __shfl_xor(p, 2, 16);
-    const float s = group_scale(p, 1.0f / 64.0f);
+    const float v0 = c0 + Q3VL_DPPF(c0, 0x102), v1 = c1 + Q3VL_DPPF(c1, 0x102);
+    const float v2 = c2 + Q3VL_DPPF(c2, 0x102), v3 = c3 + Q3VL_DPPF(c3, 0x102);
+    const float w0 = Q3VL_DPPF(v0, 0x101), w1 = Q3VL_DPPF(v1, 0x101);
+    const float w2 = Q3VL_DPPF(v2, 0x101), w3 = Q3VL_DPPF(v3, 0x101);
+    const float sumsq = Q3VL_DPPF(tree8(v0, v1, v2, v3, w0, w1, w2, w3), 0x15C);
+#undef Q3VL_DPPF
+    const float s = group_scale(sumsq, 1.0f / 64.0f);
     const float inv = rcp_rn(s);
-    const int mt = m >> 5, r = m & 31;
-    const size_t chunk0 = ((size_t)mt * Kg + g) * 4;  // 16-byte chunk index of slice 0, lane 0
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-        const int k = 16 * t + lane16;               // k inside the group
-        const int h = k >> 5, sl = (k >> 3) & 3, j = k & 7;
-        const float qv = real ? (float)quant_cvt(v[t] * inv) : 0.0f;
-        qf[((chunk0 + sl) * 64 + r + 32 * h) * 8 + j] = (_Float16)qv;
+    uint32_t q0 = quant_pair_finite(xv.x * inv, xv.y * inv);
+    uint32_t q1 = quant_pair_finite(xv.z * inv, xv.w * inv);
+    if (__builtin_expect(!__builtin_isfinite(s), 0)) {  // a non-finite group (rare)
+        q0 = quant_pair(xv.x * inv, xv.y * inv);
+        q1 = quant_pair(xv.z * inv, xv.w * inv);
     }
-    if (lane16 == 0) {
-        const int h = (r >> 2) & 1, e = 4 * (r >> 3) + (r & 3);
-        asf[(((size_t)mt * Kg + g) * 2 + h) * 16 + e] = real ? s : 0.0f;
+    // int16 pairs -> fp16 pairs (exact: |q| <= 32768 fits; rows past M: 0)
+    const uint32_t h0 = real ? __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(
+                                   (float)(int16_t)(q0 & 0xFFFF), (float)(int16_t)(q0 >> 16)))
+                             : 0u;
+    const uint32_t h1 = real ? __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(
+                                   (float)(int16_t)(q1 & 0xFFFF), (float)(int16_t)(q1 >> 16)))
+                             : 0u;
+    const int mt = m >> 5, r = m & 31;
+    const int sl = (u & 7) >> 1, hh = u >> 3;
+    const size_t piece = (((size_t)mt * Kg + g) * 4 + sl) * 64 + r + 32 * hh;  // 16-byte piece
+    *reinterpret_cast<uint2 *>(reinterpret_cast<char *>(qf) + piece * 16 + 8 * (u & 1)) = make_uint2(h0, h1);
+    if (u == 0) {
+        const int ah = (r >> 2) & 1, e = 4 * (r >> 3) + (r & 3);
+        asf[(((size_t)mt * Kg + g) * 2 + ah) * 16 + e] = real ? s : 0.0f;
     }
 }
 

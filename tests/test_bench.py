@@ -51,19 +51,26 @@ def test_reference_step_refuses_out_of_range(ref):
 
 
 def test_trace_summary(tmp_path):
+    """Regions are told apart by their markers' block count (256 threads a
+    block): 1 block = the config-1 GEMV region, 3 blocks = config 2."""
     hdr = "Kernel_Name,Grid_Size_X,Grid_Size_Y,Start_Timestamp,End_Timestamp\n"
     rows = [("gemv_kernel<A>", 128, 1, 0, 5000),
             ("swiglu_kernel", 256, 1, 10000, 11000),
             ("gemv_kernel<A>", 128, 1, 12000, 16000),
             ("gemv_kernel<A>", 128, 1, 17000, 23000),
             ("swiglu_kernel", 256, 1, 30000, 31000),
-            ("gemv_kernel<A>", 128, 1, 40000, 50000)]
+            ("gemv_kernel<A>", 128, 1, 40000, 50000),
+            ("swiglu_kernel", 768, 1, 60000, 61000),
+            ("gemm_mf_kernel<B>", 4096, 1, 62000, 64000),
+            ("swiglu_kernel", 768, 1, 70000, 71000)]
     p = tmp_path / "kt.csv"
     p.write_text(hdr + "".join(f"\"{n}\",{x},{y},{a},{b}\n" for n, x, y, a, b in rows))
     s = bench.trace_summary(str(p))
-    assert s["markers"] == 2 and s["dispatches"] == 6
-    reg = s["roofline_region"]["gemv_kernel<A> [128x1]"]
+    assert s["markers"] == 4 and s["dispatches"] == 9
+    reg = s["region cfg1_gemv"]["gemv_kernel<A> [128x1]"]
     assert reg["calls"] == 2 and reg["avg_us"] == 5.0
+    assert s["region cfg2"]["gemm_mf_kernel<B> [4096x1]"]["calls"] == 1
+    assert s["region cfg2 total_us"] == 2.0
     assert s["whole_run"]["gemv_kernel<A> [128x1]"]["calls"] == 4
 
 

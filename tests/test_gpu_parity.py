@@ -127,12 +127,16 @@ def test_gemm_parity(orc, M, N, K, gs):
                                    (17, 33000, 1024), (64, 512, 512), (300, 700, 1536), (33, 4100, 1536),
                                    (784, 3072, 1024), (196, 2048, 4096), (512, 8192, 1024),
                                    (513, 8200, 1024), (512, 2048, 6144), (1030, 8200, 128),
-                                   (1024, 8192, 256)])
+                                   (1024, 8192, 256), (784, 1024, 1024), (784, 4096, 1024),
+                                   (784, 1024, 4096), (196, 4096, 4096)])
 def test_gemm_group64_tiles_parity(orc, M, N, K):
     """The group-64 MFMA GEMMs: the fragment-order kernel (K a multiple of
     512) with one m-tile (32 x 128 tiles) or several (64 x 64 tiles), a
     single w_s tile (K = 512) and an odd number of them (K = 1536), and the
-    row-major kernel for the other K; ragged M and N, bit-exact."""
+    row-major kernel for the other K; ragged M and N, bit-exact. Every
+    vision-encoder linear at its own shape: qkv (784, 3072, 1024), proj
+    (784, 1024, 1024), fc1 (784, 4096, 1024), fc2 (784, 1024, 4096), and the
+    merger's fc1 (196, 4096, 4096) and fc2 (196, 2048, 4096)."""
     run_linear_case(orc, M, N, K, 64, seed=7 * M + N + K, groups=False)
 
 
@@ -175,7 +179,7 @@ def test_nonfinite_activation_rows_stay_nonfinite(orc):
     assert np.array_equal(np.isnan(C), np.isnan(C_ref)) and np.isnan(C).all()
 
 
-@pytest.mark.parametrize("M", [1, 3])
+@pytest.mark.parametrize("M", [1, 3, 40])
 def test_extreme_activation_groups(orc, M):
     """Groups at the edges of the quantizer. Row 0 has only finite group
     scales: squares near fp32 overflow (one element at 1.8e19, q at the
@@ -183,7 +187,8 @@ def test_extreme_activation_groups(orc, M):
     of the scale. The GEMV's fast rounding relies on that bound. Row 1 has
     infinite scales (a square that overflows, +-inf) and row 2 a NaN: the
     saturating path (INT32_MIN for NaN products). Bit-exact, NaN where the
-    oracle has NaN."""
+    oracle has NaN. M = 40 takes the fragment-order quantizer and the MFMA
+    GEMM (its non-finite groups: the saturating branch)."""
     A, W, S = make_case(6, M, 2048, 2048, 64)
     A[0, 0:64] = 1.0e18
     A[0, 5] = -1.7e18
