@@ -20,8 +20,10 @@
 //     per (activation row, weight row) [general] runs the group chain in
 //     ascending group order, exactly as the reference's scalar / AVX code.
 #include <float.h>
+#include <stdlib.h>
 
 #include <mutex>
+#include <type_traits>
 #include <vector>
 
 #include "q3vl_device.hpp"
@@ -839,6 +841,335 @@ __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), c
     }
 }
 
+// ------------------------------------------------------ streaming decode GEMV
+// The decode step's lane-path launches (one activation row, group 64, K = KC
+// of 2048 or 6144; plain / accumulate over up to three segments, or gate|up
+// with the SwiGLU epilogue; the fused RMSNorm at K = 2048), in the same
+// reference order as gemv_kernel, with each row tile one wave's work.
+//
+// A block of NW waves stages, normalizes and quantizes the activation row
+// once (quantized row and a_s into LDS, one block barrier at the end); after
+// that every wave walks its own row tiles (R rows each, stride gridDim.x*NW)
+// with no block barrier: lane t owns K-chunks t + 64i of every row (a wave's
+// load instruction reads 1 KiB of a weight row), the exact lane sums of a
+// group are reduced over the group's lane quad and written to the wave's own
+// LDS rows, and lanes 8r + j run row r's fp32 chains over the groups. The next
+// tile's weights and scales are loaded before this tile's phases, so that one
+// tile's phases run while the next tile's bytes arrive.
+template <int KC, int MD, int R, int NW>
+__global__ __launch_bounds__(64 * NW) void gemv_stream_kernel(
+    const int8_t *W0, const int8_t *W1, const int8_t *W2, const float *S0, const float *S1,
+    const float *S2, int N0, int N1, GemvArgs a, int ntiles) {
+    constexpr int GS = 64, NTH = 64 * NW;
+    constexpr int K = KC, Kg = K / GS;
+    constexpr int CPL = K / 1024;            // K-chunks per lane and weight row
+    constexpr int NQ = K / 4 / NTH;          // activation float4 per thread in the prologue
+    constexpr int HALF = R / 2;
+    constexpr int SPL = (R * Kg + 63) / 64;  // weight scales per lane and tile
+    constexpr bool SWG = MD == MD_SWIGLU;
+    constexpr int LD = (((Kg + 3) & ~3) >> 2) & 1 ? ((Kg + 3) & ~3) : ((Kg + 3) & ~3) + 4;  // group_ld(Kg)
+    constexpr bool SEGN = norm_seg(KC);
+    constexpr int NRS = norm_row_words(K, SEGN);
+    static_assert(KC == 2048 || KC == 6144, "decode row lengths");
+    static_assert(K % (4 * NTH) == 0, "whole float4 passes in the prologue");
+    static_assert(8 * R <= 64, "a tile's chains fit one wave");
+    static_assert(!SWG || R % 2 == 0, "gate and up rows in pairs");
+    static_assert(MD == MD_SWIGLU || MD == MD_RUNTIME, "plain or swiglu");
+    extern __shared__ __align__(16) unsigned char smem[];
+    __shared__ float s_norm_inv;
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+    // LDS: the quantized row (8 words per K-chunk), a_s, the fused norm's
+    // chain-major copy (K = 2048), then per wave its lane sums [8R][LD] and
+    // combined scales [R][LD]
+    uint32_t *qs = reinterpret_cast<uint32_t *>(smem);
+    float *as_l = reinterpret_cast<float *>(qs + K / 2);
+    float *xn = as_l + ((Kg + 3) & ~3);
+    int32_t *accb = reinterpret_cast<int32_t *>(xn + (KC == 2048 ? 8 * NRS : 0)) + wid * (9 * R * LD);
+    float *scb = reinterpret_cast<float *>(accb + 8 * R * LD);
+    const bool has_norm = KC == 2048 && a.norm_w != nullptr;
+
+    SegRegs sr;
+    sr.W0 = W0; sr.W1 = W1; sr.W2 = W2;
+    sr.S0 = S0; sr.S1 = S1; sr.S2 = S2;
+    sr.Y0 = a.seg[0].Y; sr.Y1 = a.seg[1].Y; sr.Y2 = a.seg[2].Y;
+    sr.N0 = N0; sr.N1 = N1; sr.N2 = a.seg[2].N;
+    int nseg = SWG ? 2 : a.nseg;
+    asm volatile("" : "+s"(sr.N0), "+s"(sr.N1), "+s"(sr.N2));
+    if constexpr (!SWG) asm volatile("" : "+s"(nseg));
+    sr.t1 = (sr.N0 + R - 1) / R;
+    sr.t2 = nseg > 2 ? sr.t1 + (sr.N1 + R - 1) / R : 0x7fffffff;
+    if (SWG || nseg < 2) sr.t1 = 0x7fffffff;
+    auto resolve = [&](int tile) {
+        Tile t;
+        if constexpr (SWG) {
+            t.tseg = 0;
+            t.tn0 = tile * HALF;
+            t.tN = sr.N0;
+        } else {
+            t.tseg = tile < sr.t1 ? 0 : (tile < sr.t2 ? 1 : 2);
+            t.tn0 = (tile - pick3(t.tseg, 0, sr.t1, sr.t2)) * R;
+            t.tN = pick3(t.tseg, sr.N0, sr.N1, sr.N2);
+        }
+        return t;
+    };
+    auto row_seg = [&](const Tile &t, int r) { return SWG ? (r < HALF ? 0 : 1) : t.tseg; };
+    auto row_n = [&](const Tile &t, int r) { return SWG ? t.tn0 + r % (HALF > 0 ? HALF : 1) : t.tn0 + r; };
+    auto row_ok = [&](const Tile &t, int r) { return row_n(t, r) < t.tN; };
+
+    // ---- one tile's weight chunks and scales into registers. Rows past the
+    // segment end read row 0 (the value is never used: no select on loaded
+    // data, so nothing waits at issue). Scales first: the scale products at
+    // the top of a tile then wait only for them (loads retire in order).
+    u32x4 wv[2][R][CPL];
+    float sv[2][SPL];
+    auto load_tile = [&](auto B, const Tile &t) {
+        constexpr int b = decltype(B)::value;
+#pragma unroll
+        for (int s = 0; s < SPL; ++s) {
+            const int e = lane + 64 * s, r = e / Kg, gg = e % Kg;
+            const bool ok = r < R && row_ok(t, r);
+            const float *S = pick3(row_seg(t, r < R ? r : 0), sr.S0, sr.S1, sr.S2);
+            sv[b][s] = S[ok ? (size_t)row_n(t, r) * Kg + gg : 0];
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int8_t *w = pick3(row_seg(t, r), sr.W0, sr.W1, sr.W2) +
+                              (size_t)(row_ok(t, r) ? row_n(t, r) : 0) * K;
+#pragma unroll
+            for (int i = 0; i < CPL; ++i)
+                wv[b][r][i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(w) + lane + 64 * i);
+        }
+    };
+
+    // ---- phase 0: the activation row (reference i8:135-177), its loads
+    // issued before the first tile's weight loads
+    float4 xv[NQ];
+#pragma unroll
+    for (int k = 0; k < NQ; ++k) xv[k] = reinterpret_cast<const float4 *>(a.A)[tid + NTH * k];
+    const int8_t *nwp = has_norm ? a.norm_w : reinterpret_cast<const int8_t *>(a.A);
+    const float *nsp = has_norm ? a.norm_s : a.A;
+    uint32_t nw4[NQ];
+    float nsc4[NQ];
+#pragma unroll
+    for (int k = 0; k < NQ; ++k) {
+        nw4[k] = has_norm ? reinterpret_cast<const uint32_t *>(nwp)[tid + NTH * k] : 0u;
+        nsc4[k] = has_norm ? nsp[(4 * (tid + NTH * k)) / GS] : 0.0f;
+    }
+    int tile = blockIdx.x * NW + wid;
+    const int stride = gridDim.x * NW;
+    // (a wave with no tile loads the last one, unused: no branch around loads)
+    Tile cur = resolve(tile < ntiles ? tile : ntiles - 1);
+    load_tile(std::integral_constant<int, 0>{}, cur);
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (KC == 2048) {
+        if (has_norm) {
+            // the chain-major copy: element 4i + c in chain 4(i & 1) + c at i/2
+#pragma unroll
+            for (int k = 0; k < NQ; ++k) {
+                const int i = tid + NTH * k, t = i >> 1;
+                float *d = xn + 4 * (i & 1) * NRS + (SEGN ? t + 4 * (t >> 5) : t);
+                d[0] = xv[k].x;
+                d[NRS] = xv[k].y;
+                d[2 * NRS] = xv[k].z;
+                d[3 * NRS] = xv[k].w;
+            }
+            lds_barrier();
+            if (tid < 64) {
+                // The sum of squares in the reference's 8-lane order: lane
+                // 8l + j holds segment j (positions 32j .. 32j+31) of chain l;
+                // in segment s only lanes j == s carry their chain, and a row
+                // shift hands each chain's sum to its next segment's lane.
+                const float *sg = xn + (tid >> 3) * NRS + (tid & 7) * 36;
+                float4 X[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) X[u] = reinterpret_cast<const float4 *>(sg)[u];
+                float acc = 0.0f;
+#pragma unroll
+                for (int sgm = 0; sgm < 8; ++sgm) {
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) {
+                        acc = fmaf(X[u].x, X[u].x, acc);
+                        acc = fmaf(X[u].y, X[u].y, acc);
+                        acc = fmaf(X[u].z, X[u].z, acc);
+                        acc = fmaf(X[u].w, X[u].w, acc);
+                    }
+                    if (sgm < 7)  // row_shr:1
+                        acc = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                                  0, __builtin_bit_cast(int, acc), 0x111, 0xF, 0xF, false));
+                }
+                // chain l's sum sits in lane 8l + 7; added in chain order
+                float ss = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, acc), 7));
+#pragma unroll
+                for (int l = 1; l < 8; ++l)
+                    ss = ss + __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, acc), 8 * l + 7));
+                if (tid == 0) s_norm_inv = rcp_rn(sqrt_rn(ss * rcp_rn((float)K) + a.norm_eps));
+            }
+            lds_barrier();
+#pragma unroll
+            for (int k = 0; k < NQ; ++k) {
+                const float comb = nsc4[k] * s_norm_inv;  // x = w * ((s_g * inv) * x)
+                const uint32_t w = nw4[k];
+                xv[k].x = (float)(int8_t)(w & 0xFF) * (comb * xv[k].x);
+                xv[k].y = (float)(int8_t)((w >> 8) & 0xFF) * (comb * xv[k].y);
+                xv[k].z = (float)(int8_t)((w >> 16) & 0xFF) * (comb * xv[k].z);
+                xv[k].w = (float)(int8_t)(w >> 24) * (comb * xv[k].w);
+            }
+        }
+    }
+    // The group quantizer in registers: float4 i of the row sits in lane
+    // i & 15 of a 16-lane row, one group per row. Chain c = 4(u & 3) + k takes
+    // elements 16t + c (step t in lane 4t + (u & 3)): each round extends the
+    // chain value of lane u - 4 (row_shr:4), so lanes 12..15 end with the 16
+    // chains; V[i] = P[i] + P[i+8] (row_shl:2), lane 12 takes lane 13's half
+    // (row_shl:1), runs the fixed tree, and the row takes lane 12's sum
+    // (row_newbcast:12).
+#define Q3VL_DPPF(v, ctrl) \
+    __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), ctrl, 0xF, 0xF, false))
+#pragma unroll
+    for (int k = 0; k < NQ; ++k) {
+        const float4 x4 = xv[k];
+        float c0 = fmaf(x4.x, x4.x, 0.0f), c1 = fmaf(x4.y, x4.y, 0.0f);
+        float c2 = fmaf(x4.z, x4.z, 0.0f), c3 = fmaf(x4.w, x4.w, 0.0f);
+#pragma unroll
+        for (int t = 1; t < 4; ++t) {
+            c0 = fmaf(x4.x, x4.x, Q3VL_DPPF(c0, 0x114));
+            c1 = fmaf(x4.y, x4.y, Q3VL_DPPF(c1, 0x114));
+            c2 = fmaf(x4.z, x4.z, Q3VL_DPPF(c2, 0x114));
+            c3 = fmaf(x4.w, x4.w, Q3VL_DPPF(c3, 0x114));
+        }
+        const float v0 = c0 + Q3VL_DPPF(c0, 0x102), v1 = c1 + Q3VL_DPPF(c1, 0x102);
+        const float v2 = c2 + Q3VL_DPPF(c2, 0x102), v3 = c3 + Q3VL_DPPF(c3, 0x102);
+        const float w0 = Q3VL_DPPF(v0, 0x101), w1 = Q3VL_DPPF(v1, 0x101);
+        const float w2 = Q3VL_DPPF(v2, 0x101), w3 = Q3VL_DPPF(v3, 0x101);
+        const float sumsq = Q3VL_DPPF(tree8(v0, v1, v2, v3, w0, w1, w2, w3), 0x15C);
+        const float sg = group_scale(sumsq, 1.0f / (float)GS);
+        const float inv = rcp_rn(sg);
+        const int i4 = tid + NTH * k;
+        if ((tid & 15) == 0) as_l[i4 >> 4] = sg;
+        uint32_t q0 = quant_pair_finite(x4.x * inv, x4.y * inv);
+        uint32_t q1 = quant_pair_finite(x4.z * inv, x4.w * inv);
+        if (__builtin_expect(!__builtin_isfinite(sg), 0)) {  // a non-finite group (rare)
+            q0 = quant_pair(x4.x * inv, x4.y * inv);
+            q1 = quant_pair(x4.z * inv, x4.w * inv);
+        }
+        reinterpret_cast<uint2 *>(qs)[i4] = make_uint2(q0, q1);
+    }
+#undef Q3VL_DPPF
+    lds_barrier();
+    // this lane's K-chunks of the quantized row (8 int16 pairs each) and the
+    // a_s of its scale elements
+    uint32_t qp[CPL][8];
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+        const u32x4 *q4 = reinterpret_cast<const u32x4 *>(qs) + 2 * (lane + 64 * i);
+        const u32x4 qa = q4[0], qb = q4[1];
+        qp[i][0] = qa.x; qp[i][1] = qa.y; qp[i][2] = qa.z; qp[i][3] = qa.w;
+        qp[i][4] = qb.x; qp[i][5] = qb.y; qp[i][6] = qb.z; qp[i][7] = qb.w;
+    }
+    float asv[SPL];
+#pragma unroll
+    for (int s = 0; s < SPL; ++s) asv[s] = as_l[(lane + 64 * s) % Kg];
+
+    const int tg = lane & 3;
+    const int cr = lane >> 3;  // the chain lane's row (lane 8r + j)
+    // One tile from buffer B; the next tile's loads go to the other buffer
+    // first. Returns false when the wave has no further tile.
+    auto step = [&](auto B) -> bool {
+        constexpr int b = decltype(B)::value;
+        const Tile t = cur;
+        const int nxt = tile + stride;
+        if (nxt < ntiles) {  // wave-uniform
+            cur = resolve(nxt);
+            load_tile(std::integral_constant<int, b ^ 1>{}, cur);
+        }
+        // ---- the combined scales fl(a_s * w_s) of the tile's rows (i8:213)
+#pragma unroll
+        for (int s = 0; s < SPL; ++s) {
+            const int e = lane + 64 * s, r = e / Kg, gg = e % Kg;
+            if (r < R) scb[r * LD + gg] = asv[s] * sv[b][s];
+        }
+        // ---- phase 1: the exact int32 lane sums of every group: the 8 lane
+        // partials of this lane's 16 bytes (weights in the high bytes: 256x),
+        // reduce-scattered over the group's lane quad; lane tg writes lanes
+        // 2tg and 2tg+1 of the group
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+#pragma unroll
+            for (int i = 0; i < CPL; ++i) {
+                const u32x4 w4 = wv[b][r][i];
+                const uint32_t wd[4] = {w4.x, w4.y, w4.z, w4.w};
+                int32_t p[8];
+#pragma unroll
+                for (int d = 0; d < 4; ++d) {
+                    p[2 * d] = dot2_z(qp[i][2 * d], lo2(wd[d]));
+                    p[2 * d + 1] = dot2_z(qp[i][2 * d + 1], hi2(wd[d]));
+                }
+                scatter_sums<4>(p, tg);
+                const int g = (lane + 64 * i) >> 2;
+                accb[(r * 8 + 2 * tg) * LD + g] = p[0] >> 8;
+                accb[(r * 8 + 2 * tg + 1) * LD + g] = p[1] >> 8;
+            }
+        }
+        // (LDS operations of one wave complete in order: the reads below see
+        // the writes above without a barrier)
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+        // ---- phase 2: lane 8r + j runs row r's chain over the groups in
+        // ascending order (i8:213-216)
+        float c = 0.0f;
+        if (lane < 8 * R) {
+            const int32_t *Lr = accb + lane * LD;
+            const float *scr = scb + cr * LD;
+#pragma unroll
+            for (int gg = 0; gg < Kg; gg += 16) {
+                int4 L4[4];
+                float4 s4[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    L4[u] = *reinterpret_cast<const int4 *>(Lr + gg + 4 * u);
+                    s4[u] = *reinterpret_cast<const float4 *>(scr + gg + 4 * u);
+                }
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    c = fmaf((float)L4[u].x, s4[u].x, c);
+                    c = fmaf((float)L4[u].y, s4[u].y, c);
+                    c = fmaf((float)L4[u].z, s4[u].z, c);
+                    c = fmaf((float)L4[u].w, s4[u].w, c);
+                }
+            }
+        }
+        // add_reduce_mm_256 over the row's 8 lanes (i8:219-222): lane j = 0
+        // ends with ((c0+c4) + (c1+c5)) + ((c2+c6) + (c3+c7))
+#define Q3VL_SHL(v, n) \
+    __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x100 + (n), 0xF, 0xF, false))
+        c = c + Q3VL_SHL(c, 4);
+        c = c + Q3VL_SHL(c, 1);
+        c = c + Q3VL_SHL(c, 2);
+#undef Q3VL_SHL
+        // ---- epilogue
+        const bool yvalid = lane < 8 * R && (lane & 7) == 0 && row_ok(t, cr);
+        if constexpr (SWG) {
+            // the up row of gate row r is row r + HALF, 8 * HALF lanes above
+            const float up = __shfl_down(c, 8 * HALF);
+            if (yvalid && cr < HALF) sr.Y0[row_n(t, cr)] = silu_mul(c, up);
+        } else {
+            if (yvalid) {
+                float *dst = pick3(t.tseg, sr.Y0, sr.Y1, sr.Y2) + row_n(t, cr);
+                *dst = a.accumulate ? *dst + c : c;  // add_vector: to[i] += from[i]
+            }
+        }
+        // the next tile rewrites this wave's LDS rows after the reads above
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+        tile = nxt;
+        return nxt < ntiles;
+    };
+    if (tile < ntiles) {
+        while (step(std::integral_constant<int, 0>{}) && step(std::integral_constant<int, 1>{})) {
+        }
+    }
+}
+
 __device__ void am_block_reduce(float &bv, int32_t &bi) {
     __shared__ float sv[256];
     __shared__ int32_t si[256];
@@ -1085,9 +1416,109 @@ static int lane_rows_sub(const GemvArgs &a, int cus) {
     return 0;
 }
 
+
+// ---- the streaming decode GEMV's launch
+struct StreamCfg {
+    int nw, r;  // waves per block, rows per wave tile (0: not taken)
+    int bpc;    // blocks per CU at most, 0: one tile per wave (else the waves loop over tiles)
+};
+
+// Measured at the decode shapes (graph replay of 20 launches, same weights,
+// MI355X; us per launch, gemv_kernel's in brackets):
+//   q|k|v   K = 2048, 4096 rows:  8 waves, 2 rows, 256 blocks      3.83 (4.24)
+//   o       K = 2048, 2048 rows:  8 waves, 1 row, 256 blocks       3.33 (3.71)
+//   gate|up K = 2048, 2 x 6144:   8 waves, 1+1 rows, 2 blocks/CU   6.02 (6.29)
+//   down    K = 6144, 2048 rows:  8 waves, 1 row, 256 blocks       5.93 (6.02)
+// (An empty kernel costs 2.2 us per launch in the same replay.)
+static StreamCfg stream_cfg(const GemvArgs &a) {
+    if (a.mode == GEMV_SWIGLU) return {8, 2, 2};
+    if (a.K == 6144) return {8, 1, 0};
+    int rows = 0;
+    for (int s = 0; s < a.nseg; ++s) rows += a.seg[s].N;
+    return rows > 2048 ? StreamCfg{8, 2, 0} : StreamCfg{8, 1, 0};
+}
+
+static size_t stream_lds(int KC, int R, int NW) {
+    const int Kg = KC / 64, ld = group_ld(Kg);
+    return (size_t)4 * (KC / 2 + ((Kg + 3) & ~3) + (KC == 2048 ? 8 * norm_row_words(KC, norm_seg(KC)) : 0) +
+                        NW * 9 * R * ld);
+}
+
+template <int KC, int MD, int R, int NW>
+static hipError_t launch_stream_t(const GemvArgs &a, int bpc, int *grid_out, hipStream_t st) {
+    int ntiles = 0;
+    if (MD == MD_SWIGLU) {
+        ntiles = (a.seg[0].N + R / 2 - 1) / (R / 2);
+    } else {
+        for (int s = 0; s < a.nseg; ++s) ntiles += (a.seg[s].N + R - 1) / R;
+    }
+    if (ntiles < 1) return hipSuccess;
+    int dev = 0, cus = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e == hipSuccess) e = device_cus(dev, &cus);
+    if (e != hipSuccess) return e;
+    int grid = (ntiles + NW - 1) / NW;
+    if (bpc > 0 && grid > bpc * cus) grid = bpc * cus;
+    if (grid_out) *grid_out = grid;
+    // (K = 6144 with 8 waves of 2 rows needs more than the default 64 KiB)
+    static const hipError_t attr = hipFuncSetAttribute(
+        reinterpret_cast<const void *>(&gemv_stream_kernel<KC, MD, R, NW>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, (int)stream_lds(KC, R, NW));
+    if (attr != hipSuccess) return attr;
+    gemv_stream_kernel<KC, MD, R, NW><<<grid, 64 * NW, stream_lds(KC, R, NW), st>>>(
+        a.seg[0].W, a.seg[1].W, a.seg[2].W, a.seg[0].S, a.seg[1].S, a.seg[2].S, a.seg[0].N, a.seg[1].N, a,
+        ntiles);
+    return hipGetLastError();
+}
+
+template <int KC, int MD>
+static hipError_t launch_stream_md(const GemvArgs &a, const StreamCfg &c, int *grid_out, hipStream_t st) {
+#define Q3VL_STREAM(R_, NW_) \
+    if (c.r == R_ && c.nw == NW_) return launch_stream_t<KC, MD, R_, NW_>(a, c.bpc, grid_out, st);
+    if constexpr (MD != MD_SWIGLU) {
+        Q3VL_STREAM(1, 4)
+        Q3VL_STREAM(1, 8)
+    }
+    Q3VL_STREAM(2, 4)
+    Q3VL_STREAM(2, 8)
+    if constexpr (KC == 2048) {  // (4 rows of 6144 bytes, double-buffered, exceed the registers)
+        Q3VL_STREAM(4, 4)
+        Q3VL_STREAM(4, 8)
+    }
+#undef Q3VL_STREAM
+    return hipErrorInvalidValue;
+}
+
+// Whether the streaming kernel takes this lane-path launch: one activation
+// row, group 64, K of 2048 or 6144, plain or swiglu, no group-sum output.
+// Q3VL_GEMV_STREAM=0 in the environment keeps every launch on gemv_kernel.
+static bool stream_takes(const GemvArgs &a) {
+    static const bool enabled = [] {
+        const char *v = getenv("Q3VL_GEMV_STREAM");
+        return !(v && v[0] == '0');
+    }();
+    if (!enabled || a.M != 1 || a.gs != 64 || (a.K != 2048 && a.K != 6144)) return false;
+    if (a.mode != GEMV_PLAIN && a.mode != GEMV_SWIGLU) return false;
+    // (gate|up stays on gemv_kernel: 8.0 us against 7.4 inside the decode step)
+    if (a.mode == GEMV_SWIGLU) return false;
+    if (a.norm_w && a.K != 2048) return false;
+    for (int s = 0; s < a.nseg; ++s)
+        if (a.seg[s].G) return false;
+    return true;
+}
+
+static hipError_t launch_stream(const GemvArgs &a, int *grid_out, hipStream_t st) {
+    const StreamCfg c = stream_cfg(a);
+    if (a.K == 2048)
+        return a.mode == GEMV_SWIGLU ? launch_stream_md<2048, MD_SWIGLU>(a, c, grid_out, st)
+                                     : launch_stream_md<2048, MD_RUNTIME>(a, c, grid_out, st);
+    return launch_stream_md<6144, MD_RUNTIME>(a, c, grid_out, st);
+}
+
 template <int GS>
 static hipError_t launch_gemv_gs(const GemvArgs &a, bool lanes, int *grid_out, hipStream_t st) {
     if (lanes) {
+        if (GS == 64 && stream_takes(a)) return launch_stream(a, grid_out, st);
         if (GS == 64 && a.K == 2048) {
             int dev = 0, cus = 0;
             hipError_t e = hipGetDevice(&dev);

@@ -112,6 +112,19 @@ def test_lane_gemv_parity(orc, M, N, K, gs):
     run_linear_case(orc, M, N, K, gs, seed=N + K + gs, groups=N <= 8192)
 
 
+# The decode step's row lengths at group 64 without group-sum output: the
+# streaming kernel (one wave per row tile, tiles looped per wave), with ragged
+# last tiles and more tiles than waves.
+STREAM = [(1, 1024, 2048), (1, 1029, 2048), (1, 2050, 2048), (1, 4096, 2048), (1, 9001, 2048),
+          (1, 1024, 6144), (1, 1031, 6144), (1, 2048, 6144), (1, 6145, 6144)]
+
+
+@pytest.mark.parametrize("M,N,K", STREAM, ids=[str(c) for c in STREAM])
+def test_stream_gemv_parity(orc, M, N, K):
+    assert q.uses_lane_path(M, N, K)
+    run_linear_case(orc, M, N, K, 64, seed=3 * N + K, groups=False)
+
+
 @pytest.mark.parametrize("M,N,K,gs", GENERAL, ids=[str(c) for c in GENERAL])
 def test_general_gemv_parity(orc, M, N, K, gs):
     assert not q.uses_lane_path(M, N, K)
