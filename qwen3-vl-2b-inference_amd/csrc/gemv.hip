@@ -847,15 +847,17 @@ __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), c
 // with the SwiGLU epilogue; the fused RMSNorm at K = 2048), in the same
 // reference order as gemv_kernel, with each row tile one wave's work.
 //
-// A block of NW waves stages, normalizes and quantizes the activation row
-// once (quantized row and a_s into LDS, one block barrier at the end); after
-// that every wave walks its own row tiles (R rows each, stride gridDim.x*NW)
-// with no block barrier: lane t owns K-chunks t + 64i of every row (a wave's
-// load instruction reads 1 KiB of a weight row), the exact lane sums of a
-// group are reduced over the group's lane quad and written to the wave's own
-// LDS rows, and lanes 8r + j run row r's fp32 chains over the groups. The next
-// tile's weights and scales are loaded before this tile's phases, so that one
-// tile's phases run while the next tile's bytes arrive.
+// Prologue (once per block): the activation row is normalized (fused norm)
+// and quantized, 8 lanes per group, into LDS; one block barrier. After it
+// every wave walks its own row tiles (R rows each, stride gridDim.x*NW) with
+// no block barrier. A tile's R*Kg (row, group) pairs are taken 64 at a time
+// ("passes"), one per lane: the lane loads the group's 64 weight bytes (four
+// 16-byte loads) and accumulates the 8 exact int32 lane sums of the group
+// (i8:188-211) with v_dot2 -- no cross-lane reduction -- and writes them as
+// floats, with the combined scale fl(a_s * w_s), to the wave's own LDS rows.
+// Then lanes 8r + j run row r's fp32 chains over the groups (i8:213-216) and
+// the 8-lane tree (i8:219-222). The next tile's weights and scales are loaded
+// before this tile's phases.
 template <int KC, int MD, int R, int NW>
 __global__ __launch_bounds__(64 * NW) void gemv_stream_kernel(
     const int8_t *W0, const int8_t *W1, const int8_t *W2, const float *S0, const float *S1,
@@ -863,15 +865,14 @@ __global__ __launch_bounds__(64 * NW) void gemv_stream_kernel(
     constexpr int GS = 64, NTH = 64 * NW;
     constexpr int K = KC, Kg = K / GS;
     constexpr int CPL = K / 1024;            // K-chunks per lane and weight row
-    constexpr int NQ = K / 4 / NTH;          // activation float4 per thread in the prologue
-    constexpr int HALF = R / 2;
     constexpr int SPL = (R * Kg + 63) / 64;  // weight scales per lane and tile
+    constexpr int HALF = R / 2;
     constexpr bool SWG = MD == MD_SWIGLU;
     constexpr int LD = (((Kg + 3) & ~3) >> 2) & 1 ? ((Kg + 3) & ~3) : ((Kg + 3) & ~3) + 4;  // group_ld(Kg)
+    constexpr int QLD = 36;  // words per group of the quantized row (32 + 4 padding)
     constexpr bool SEGN = norm_seg(KC);
     constexpr int NRS = norm_row_words(K, SEGN);
     static_assert(KC == 2048 || KC == 6144, "decode row lengths");
-    static_assert(K % (4 * NTH) == 0, "whole float4 passes in the prologue");
     static_assert(8 * R <= 64, "a tile's chains fit one wave");
     static_assert(!SWG || R % 2 == 0, "gate and up rows in pairs");
     static_assert(MD == MD_SWIGLU || MD == MD_RUNTIME, "plain or swiglu");
@@ -880,14 +881,14 @@ __global__ __launch_bounds__(64 * NW) void gemv_stream_kernel(
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
-    // LDS: the quantized row (8 words per K-chunk), a_s, the fused norm's
+    // LDS: the quantized row ([Kg][QLD] words), a_s, the fused norm's
     // chain-major copy (K = 2048), then per wave its lane sums [8R][LD] and
     // combined scales [R][LD]
     uint32_t *qs = reinterpret_cast<uint32_t *>(smem);
-    float *as_l = reinterpret_cast<float *>(qs + K / 2);
+    float *as_l = reinterpret_cast<float *>(qs + Kg * QLD);
     float *xn = as_l + ((Kg + 3) & ~3);
-    int32_t *accb = reinterpret_cast<int32_t *>(xn + (KC == 2048 ? 8 * NRS : 0)) + wid * (9 * R * LD);
-    float *scb = reinterpret_cast<float *>(accb + 8 * R * LD);
+    float *accb = xn + (KC == 2048 ? 8 * NRS : 0) + wid * (9 * R * LD);
+    float *scb = accb + 8 * R * LD;
     const bool has_norm = KC == 2048 && a.norm_w != nullptr;
 
     SegRegs sr;
@@ -943,37 +944,56 @@ __global__ __launch_bounds__(64 * NW) void gemv_stream_kernel(
         }
     };
 
-    // ---- phase 0: the activation row (reference i8:135-177), its loads
-    // issued before the first tile's weight loads
-    float4 xv[NQ];
-#pragma unroll
-    for (int k = 0; k < NQ; ++k) xv[k] = reinterpret_cast<const float4 *>(a.A)[tid + NTH * k];
-    const int8_t *nwp = has_norm ? a.norm_w : reinterpret_cast<const int8_t *>(a.A);
-    const float *nsp = has_norm ? a.norm_s : a.A;
-    uint32_t nw4[NQ];
-    float nsc4[NQ];
-#pragma unroll
-    for (int k = 0; k < NQ; ++k) {
-        nw4[k] = has_norm ? reinterpret_cast<const uint32_t *>(nwp)[tid + NTH * k] : 0u;
-        nsc4[k] = has_norm ? nsp[(4 * (tid + NTH * k)) / GS] : 0.0f;
-    }
     int tile = blockIdx.x * NW + wid;
     const int stride = gridDim.x * NW;
     // (a wave with no tile loads the last one, unused: no branch around loads)
     Tile cur = resolve(tile < ntiles ? tile : ntiles - 1);
+
+    // ---- phase 0 (i8:135-177): the group quantizer, 8 lanes a group. Lane
+    // u of group g holds elements 64g + 16t + 2u + k (t = 0..3, k = 0, 1),
+    // i.e. chains 2u and 2u + 1 of the group's 16 sum-of-squares chains
+    // (chain c takes elements 16t + c in ascending t). Its loads are issued
+    // before the first tile's weight loads, so waiting for them does not wait
+    // for the weights.
+    constexpr int QIT = (8 * Kg + NTH - 1) / NTH;  // quantizer passes (whole waves)
+    float2 xq[QIT][4];
+    uint32_t nwq[QIT][4];
+    float nsq[QIT];
+#pragma unroll
+    for (int it = 0; it < QIT; ++it) {
+        const int qi = tid + NTH * it;
+        if (qi < 8 * Kg) {  // wave-uniform
+            const int g = qi >> 3, u = qi & 7;
+            const float *xg = a.A + 64 * g + 2 * u;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) xq[it][t] = *reinterpret_cast<const float2 *>(xg + 16 * t);
+            if (has_norm) {
+                const int8_t *nw = a.norm_w + 64 * g + 2 * u;
+#pragma unroll
+                for (int t = 0; t < 4; ++t) nwq[it][t] = *reinterpret_cast<const uint16_t *>(nw + 16 * t);
+                nsq[it] = a.norm_s[g];
+            }
+        }
+    }
     load_tile(std::integral_constant<int, 0>{}, cur);
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (KC == 2048) {
+        static_assert(KC != 2048 || QIT == 1, "one quantizer pass at K = 2048");
         if (has_norm) {
-            // the chain-major copy: element 4i + c in chain 4(i & 1) + c at i/2
+            // the fused norm's inverse rms: the row into the chain-major copy
+            // (element e in chain e % 8 at e / 8), then the 8-chain sum of
+            // squares
+            if (tid < 8 * Kg) {
+                const int g = tid >> 3, u = tid & 7;
 #pragma unroll
-            for (int k = 0; k < NQ; ++k) {
-                const int i = tid + NTH * k, t = i >> 1;
-                float *d = xn + 4 * (i & 1) * NRS + (SEGN ? t + 4 * (t >> 5) : t);
-                d[0] = xv[k].x;
-                d[NRS] = xv[k].y;
-                d[2 * NRS] = xv[k].z;
-                d[3 * NRS] = xv[k].w;
+                for (int t = 0; t < 4; ++t) {
+#pragma unroll
+                    for (int k = 0; k < 2; ++k) {
+                        const int l = (2 * u + k) & 7;
+                        const int pos = 8 * g + 2 * t + ((2 * u + k) >> 3);
+                        xn[l * NRS + (SEGN ? pos + 4 * (pos >> 5) : pos)] = k ? xq[0][t].y : xq[0][t].x;
+                    }
+                }
             }
             lds_barrier();
             if (tid < 64) {
@@ -1007,63 +1027,66 @@ __global__ __launch_bounds__(64 * NW) void gemv_stream_kernel(
                 if (tid == 0) s_norm_inv = rcp_rn(sqrt_rn(ss * rcp_rn((float)K) + a.norm_eps));
             }
             lds_barrier();
+            if (tid < 8 * Kg) {
+                const float comb = nsq[0] * s_norm_inv;  // x = w * ((s_g * inv) * x)
 #pragma unroll
-            for (int k = 0; k < NQ; ++k) {
-                const float comb = nsc4[k] * s_norm_inv;  // x = w * ((s_g * inv) * x)
-                const uint32_t w = nw4[k];
-                xv[k].x = (float)(int8_t)(w & 0xFF) * (comb * xv[k].x);
-                xv[k].y = (float)(int8_t)((w >> 8) & 0xFF) * (comb * xv[k].y);
-                xv[k].z = (float)(int8_t)((w >> 16) & 0xFF) * (comb * xv[k].z);
-                xv[k].w = (float)(int8_t)(w >> 24) * (comb * xv[k].w);
+                for (int t = 0; t < 4; ++t) {
+                    xq[0][t].x = (float)(int8_t)(nwq[0][t] & 0xFF) * (comb * xq[0][t].x);
+                    xq[0][t].y = (float)(int8_t)(nwq[0][t] >> 8) * (comb * xq[0][t].y);
+                }
             }
         }
     }
-    // The group quantizer in registers: float4 i of the row sits in lane
-    // i & 15 of a 16-lane row, one group per row. Chain c = 4(u & 3) + k takes
-    // elements 16t + c (step t in lane 4t + (u & 3)): each round extends the
-    // chain value of lane u - 4 (row_shr:4), so lanes 12..15 end with the 16
-    // chains; V[i] = P[i] + P[i+8] (row_shl:2), lane 12 takes lane 13's half
-    // (row_shl:1), runs the fixed tree, and the row takes lane 12's sum
-    // (row_newbcast:12).
+    // The quantizer proper. V[i] = P[i] + P[i+8] (lane u < 4 takes lane u + 4:
+    // row_shl:4), then the fixed tree ((V0+V4)+(V1+V5)) + ((V2+V6)+(V3+V7))
+    // over lanes 0..3 (row_shl:2, row_shl:1), broadcast from the group's
+    // lane 0.
 #define Q3VL_DPPF(v, ctrl) \
     __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), ctrl, 0xF, 0xF, false))
 #pragma unroll
-    for (int k = 0; k < NQ; ++k) {
-        const float4 x4 = xv[k];
-        float c0 = fmaf(x4.x, x4.x, 0.0f), c1 = fmaf(x4.y, x4.y, 0.0f);
-        float c2 = fmaf(x4.z, x4.z, 0.0f), c3 = fmaf(x4.w, x4.w, 0.0f);
+    for (int it = 0; it < QIT; ++it) {
+        const int qi = tid + NTH * it;
+        if (qi >= 8 * Kg) break;  // wave-uniform
+        const int g = qi >> 3, u = qi & 7;
+        const float2 *xv = xq[it];
+        float c0 = fmaf(xv[0].x, xv[0].x, 0.0f), c1 = fmaf(xv[0].y, xv[0].y, 0.0f);
 #pragma unroll
         for (int t = 1; t < 4; ++t) {
-            c0 = fmaf(x4.x, x4.x, Q3VL_DPPF(c0, 0x114));
-            c1 = fmaf(x4.y, x4.y, Q3VL_DPPF(c1, 0x114));
-            c2 = fmaf(x4.z, x4.z, Q3VL_DPPF(c2, 0x114));
-            c3 = fmaf(x4.w, x4.w, Q3VL_DPPF(c3, 0x114));
+            c0 = fmaf(xv[t].x, xv[t].x, c0);
+            c1 = fmaf(xv[t].y, xv[t].y, c1);
         }
-        const float v0 = c0 + Q3VL_DPPF(c0, 0x102), v1 = c1 + Q3VL_DPPF(c1, 0x102);
-        const float v2 = c2 + Q3VL_DPPF(c2, 0x102), v3 = c3 + Q3VL_DPPF(c3, 0x102);
-        const float w0 = Q3VL_DPPF(v0, 0x101), w1 = Q3VL_DPPF(v1, 0x101);
-        const float w2 = Q3VL_DPPF(v2, 0x101), w3 = Q3VL_DPPF(v3, 0x101);
-        const float sumsq = Q3VL_DPPF(tree8(v0, v1, v2, v3, w0, w1, w2, w3), 0x15C);
+        const float s0 = c0 + Q3VL_DPPF(c0, 0x104), s1 = c1 + Q3VL_DPPF(c1, 0x104);
+        const float y0 = s0 + Q3VL_DPPF(s0, 0x102), y1 = s1 + Q3VL_DPPF(s1, 0x102);
+        const float z = y0 + y1;
+        const float sum = z + Q3VL_DPPF(z, 0x101);
+        // lane 0 of the quad to the quad, then lanes 4..7 take lanes 0..3
+        // (row_shr:4 on banks 1 and 3 only)
+        const int b0 = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sum), 0x00, 0xF, 0xF, false);
+        const float sumsq = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(b0, b0, 0x114, 0xF, 0xA, false));
         const float sg = group_scale(sumsq, 1.0f / (float)GS);
         const float inv = rcp_rn(sg);
-        const int i4 = tid + NTH * k;
-        if ((tid & 15) == 0) as_l[i4 >> 4] = sg;
-        uint32_t q0 = quant_pair_finite(x4.x * inv, x4.y * inv);
-        uint32_t q1 = quant_pair_finite(x4.z * inv, x4.w * inv);
+        if (u == 0) as_l[g] = sg;
+        uint32_t q[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) q[t] = quant_pair_finite(xv[t].x * inv, xv[t].y * inv);
         if (__builtin_expect(!__builtin_isfinite(sg), 0)) {  // a non-finite group (rare)
-            q0 = quant_pair(x4.x * inv, x4.y * inv);
-            q1 = quant_pair(x4.z * inv, x4.w * inv);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) q[t] = quant_pair(xv[t].x * inv, xv[t].y * inv);
         }
-        reinterpret_cast<uint2 *>(qs)[i4] = make_uint2(q0, q1);
+        // pair 8t + u of the group
+#pragma unroll
+        for (int t = 0; t < 4; ++t) qs[QLD * g + 8 * t + u] = q[t];
     }
 #undef Q3VL_DPPF
     lds_barrier();
+
     // this lane's K-chunks of the quantized row (8 int16 pairs each) and the
     // a_s of its scale elements
     uint32_t qp[CPL][8];
 #pragma unroll
     for (int i = 0; i < CPL; ++i) {
-        const u32x4 *q4 = reinterpret_cast<const u32x4 *>(qs) + 2 * (lane + 64 * i);
+        const int ch = lane + 64 * i;  // K-chunk: group ch / 4, pairs 8 (ch % 4) ..
+        const u32x4 *q4 = reinterpret_cast<const u32x4 *>(qs + QLD * (ch >> 2) + 8 * (ch & 3));
         const u32x4 qa = q4[0], qb = q4[1];
         qp[i][0] = qa.x; qp[i][1] = qa.y; qp[i][2] = qa.z; qp[i][3] = qa.w;
         qp[i][4] = qb.x; qp[i][5] = qb.y; qp[i][6] = qb.z; qp[i][7] = qb.w;
@@ -1108,8 +1131,8 @@ __global__ __launch_bounds__(64 * NW) void gemv_stream_kernel(
                 }
                 scatter_sums<4>(p, tg);
                 const int g = (lane + 64 * i) >> 2;
-                accb[(r * 8 + 2 * tg) * LD + g] = p[0] >> 8;
-                accb[(r * 8 + 2 * tg + 1) * LD + g] = p[1] >> 8;
+                accb[(r * 8 + 2 * tg) * LD + g] = (float)(p[0] >> 8);
+                accb[(r * 8 + 2 * tg + 1) * LD + g] = (float)(p[1] >> 8);
             }
         }
         // (LDS operations of one wave complete in order: the reads below see
@@ -1119,23 +1142,22 @@ __global__ __launch_bounds__(64 * NW) void gemv_stream_kernel(
         // ascending order (i8:213-216)
         float c = 0.0f;
         if (lane < 8 * R) {
-            const int32_t *Lr = accb + lane * LD;
+            const float *Lr = accb + lane * LD;
             const float *scr = scb + cr * LD;
 #pragma unroll
             for (int gg = 0; gg < Kg; gg += 16) {
-                int4 L4[4];
-                float4 s4[4];
+                float4 L4[4], s4[4];
 #pragma unroll
                 for (int u = 0; u < 4; ++u) {
-                    L4[u] = *reinterpret_cast<const int4 *>(Lr + gg + 4 * u);
+                    L4[u] = *reinterpret_cast<const float4 *>(Lr + gg + 4 * u);
                     s4[u] = *reinterpret_cast<const float4 *>(scr + gg + 4 * u);
                 }
 #pragma unroll
                 for (int u = 0; u < 4; ++u) {
-                    c = fmaf((float)L4[u].x, s4[u].x, c);
-                    c = fmaf((float)L4[u].y, s4[u].y, c);
-                    c = fmaf((float)L4[u].z, s4[u].z, c);
-                    c = fmaf((float)L4[u].w, s4[u].w, c);
+                    c = fmaf(L4[u].x, s4[u].x, c);
+                    c = fmaf(L4[u].y, s4[u].y, c);
+                    c = fmaf(L4[u].z, s4[u].z, c);
+                    c = fmaf(L4[u].w, s4[u].w, c);
                 }
             }
         }
@@ -1423,15 +1445,18 @@ struct StreamCfg {
     int bpc;    // blocks per CU at most, 0: one tile per wave (else the waves loop over tiles)
 };
 
-// Measured at the decode shapes (graph replay of 20 launches, same weights,
-// MI355X; us per launch, gemv_kernel's in brackets):
-//   q|k|v   K = 2048, 4096 rows:  8 waves, 2 rows, 256 blocks      3.83 (4.24)
-//   o       K = 2048, 2048 rows:  8 waves, 1 row, 256 blocks       3.33 (3.71)
-//   gate|up K = 2048, 2 x 6144:   8 waves, 1+1 rows, 2 blocks/CU   6.02 (6.29)
-//   down    K = 6144, 2048 rows:  8 waves, 1 row, 256 blocks       5.93 (6.02)
-// (An empty kernel costs 2.2 us per launch in the same replay.)
+// Measured at the decode shapes (MI355X, us per launch: a HIP graph of one
+// launch per weight copy, with more than 640 MB of copies so that every
+// launch streams its weights from HBM, as in the decode step; gemv_kernel's
+// in brackets):
+//   q|k|v   K = 2048, 4096 rows:  8 waves, 2 rows, 256 blocks      4.11 (4.38)
+//   o       K = 2048, 2048 rows:  8 waves, 1 row, 256 blocks       3.26 (3.42)
+//   gate|up K = 2048, 2 x 6144:   4 waves, 2+2 rows, 768 blocks    7.39 (7.61)
+//   down    K = 6144, 2048 rows:  8 waves, 1 row, 256 blocks       5.37 (6.34)
+// Plain reads of the same bytes from HBM in the same replay take 2.2 (4 MB),
+// 2.8 (8 MB), 3.8 (12 MB) and 5.4 us (24 MB); an empty kernel 2.2 us.
 static StreamCfg stream_cfg(const GemvArgs &a) {
-    if (a.mode == GEMV_SWIGLU) return {8, 2, 2};
+    if (a.mode == GEMV_SWIGLU) return {4, 4, 0};
     if (a.K == 6144) return {8, 1, 0};
     int rows = 0;
     for (int s = 0; s < a.nseg; ++s) rows += a.seg[s].N;
@@ -1440,7 +1465,7 @@ static StreamCfg stream_cfg(const GemvArgs &a) {
 
 static size_t stream_lds(int KC, int R, int NW) {
     const int Kg = KC / 64, ld = group_ld(Kg);
-    return (size_t)4 * (KC / 2 + ((Kg + 3) & ~3) + (KC == 2048 ? 8 * norm_row_words(KC, norm_seg(KC)) : 0) +
+    return (size_t)4 * (36 * Kg + ((Kg + 3) & ~3) + (KC == 2048 ? 8 * norm_row_words(KC, norm_seg(KC)) : 0) +
                         NW * 9 * R * ld);
 }
 
@@ -1499,8 +1524,7 @@ static bool stream_takes(const GemvArgs &a) {
     }();
     if (!enabled || a.M != 1 || a.gs != 64 || (a.K != 2048 && a.K != 6144)) return false;
     if (a.mode != GEMV_PLAIN && a.mode != GEMV_SWIGLU) return false;
-    // (gate|up stays on gemv_kernel: 8.0 us against 7.4 inside the decode step)
-    if (a.mode == GEMV_SWIGLU) return false;
+    if (a.mode == GEMV_SWIGLU && (a.nseg != 2 || a.K != 2048)) return false;
     if (a.norm_w && a.K != 2048) return false;
     for (int s = 0; s < a.nseg; ++s)
         if (a.seg[s].G) return false;
