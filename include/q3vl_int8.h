@@ -180,7 +180,9 @@ typedef struct q3vl_text_model {
      * chunk. It differs from the reference order by the error of the
      * reference's exp256 polynomial (up to a few 1e-4 of the output scale;
      * each order is that far from an exact softmax), and the test oracle
-     * restates it exactly. */
+     * restates it exactly. It zeroes a head exactly where the reference
+     * does (some score's exp256(s - M) is -inf): each chunk keeps its
+     * smallest finite score for that check. */
     int attn_order;
 } q3vl_text_model;
 

@@ -274,13 +274,17 @@ void orc_attention(const float *q, const float *kc, const float *vc, size_t head
  * then, over the chunks ascending: M = max_c m_c, w_c = exp256(m_c - M) (0
  * for m_c = -inf or M not finite), L and O[d] fmaf chains of w_c * l_c and
  * w_c * o_c[d], out[d] = O[d] * (1.0f / L) when L is finite and positive,
- * else 0. */
+ * else 0. The whole head is 0 when M is finite and exp256(min_c - M) is -inf
+ * for some chunk, min_c being the chunk's smallest score above -inf: the
+ * reference's softmax has a -inf term exactly then (exp256 is -inf on a
+ * half-line, fl(s - M) is monotone in s) and zeroes the head
+ * (text_layer.cpp:512-515). */
 void orc_attention_chunked(const float *q, const float *kc, const float *vc, size_t heads,
                            size_t kv_heads, size_t hd, size_t max_seq, size_t pos, float *att,
                            float *out) {
     const size_t kv_mul = heads / kv_heads, n = pos + 1, nch = (n + 63) / 64;
     const float inv_sqrt_d = 1.0f / sqrtf((float)hd);
-    float *mc = malloc(nch * 4), *lc = malloc(nch * 4), *oc = malloc(nch * hd * 4);
+    float *mc = malloc(nch * 4), *lc = malloc(nch * 4), *nc = malloc(nch * 4), *oc = malloc(nch * hd * 4);
     for (size_t h = 0; h < heads; ++h) {
         const float *qh = q + h * hd;
         const float *kh = kc + (h / kv_mul) * max_seq * hd;
@@ -290,8 +294,12 @@ void orc_attention_chunked(const float *q, const float *kc, const float *vc, siz
             att[t] = dot_tail(qh, kh + t * hd, hd) * inv_sqrt_d;
         for (size_t c = 0; c < nch; ++c) {
             const size_t t0 = 64 * c, rows = n - t0 < 64 ? n - t0 : 64;
-            float m = -INFINITY;
-            for (size_t i = 0; i < rows; ++i) m = fmaxf(m, att[t0 + i]);
+            float m = -INFINITY, mn = INFINITY;
+            for (size_t i = 0; i < rows; ++i) {
+                m = fmaxf(m, att[t0 + i]);
+                if (att[t0 + i] > -INFINITY) mn = fminf(mn, att[t0 + i]);
+            }
+            nc[c] = mn;
             float e[64];
             for (size_t i = 0; i < 64; ++i)
                 e[i] = (i < rows && att[t0 + i] > -INFINITY && isfinite(m))
@@ -313,7 +321,14 @@ void orc_attention_chunked(const float *q, const float *kc, const float *vc, siz
         }
         float M = -INFINITY;
         for (size_t c = 0; c < nch; ++c) M = fmaxf(M, mc[c]);
+        int vanish = 0;
+        for (size_t c = 0; c < nch; ++c)
+            if (isfinite(M) && nc[c] < INFINITY && orc_exp256(nc[c] - M) == -INFINITY) vanish = 1;
         for (size_t d = 0; d < hd; ++d) {
+            if (vanish) {
+                out[h * hd + d] = 0.0f;
+                continue;
+            }
             float L = 0.0f, O = 0.0f;
             for (size_t c = 0; c < nch; ++c) {
                 const float w = (isfinite(M) && mc[c] > -INFINITY) ? orc_exp256(mc[c] - M) : 0.0f;
@@ -323,7 +338,7 @@ void orc_attention_chunked(const float *q, const float *kc, const float *vc, siz
             out[h * hd + d] = (L > 0.0f && isfinite(L)) ? O * (1.0f / L) : 0.0f;
         }
     }
-    free(mc), free(lc), free(oc);
+    free(mc), free(lc), free(nc), free(oc);
 }
 
 /* model/src/forward.cpp:458-720 forward_text for a text token at `pos`.

@@ -188,8 +188,8 @@ int run_linear(const float *A, int nseg, const int8_t *const *W, const float *co
     if (M == 0 || Nmax == 0) return Q3VL_OK;
     if (K == 0) {  // the reference's general path leaves C = 0 (and argmax 0)
         for (int i = 0; i < nseg; ++i)
-            if (C[i]) Q3VL_HIP(hipMemsetAsync(C[i], 0, M * Ns[i] * 4, st), "hipMemsetAsync(C)");
-        if (ids) Q3VL_HIP(hipMemsetAsync(ids, 0, M * 4, st), "hipMemsetAsync(ids)");
+            if (C[i]) Q3VL_HIP(launch_zero_words(C[i], M * Ns[i], st), "zero fill (C)");
+        if (ids) Q3VL_HIP(launch_zero_words(ids, M, st), "zero fill (ids)");
         return Q3VL_OK;
     }
     const WsLayout L = layout(M, Nmax, K, gs);
@@ -405,7 +405,7 @@ DecodeLayout decode_layout(const q3vl_text_model *m) {
     // the chunked attention order's per-chunk partials
     const bool chunked = m->attn_order == Q3VL_ATTN_CHUNKED;
     L.part_o = chunked ? take(NH * (size_t)L.max_chunks * D * 4) : 0;
-    L.part_ml = chunked ? take(NH * (size_t)L.max_chunks * 2 * 4) : 0;
+    L.part_ml = chunked ? take(NH * (size_t)L.max_chunks * 4 * 4) : 0;  // (m, l, min, 0) per chunk
     L.total = off;
     return L;
 }

@@ -102,6 +102,18 @@ __device__ __forceinline__ float wave_max(float v) {
     return fmaxf(fmaxf(readlane_f(v, 0), readlane_f(v, 16)), fmaxf(readlane_f(v, 32), readlane_f(v, 48)));
 }
 
+// Minimum over the 64 lanes, wave-uniform (the same moves as wave_max).
+__device__ __forceinline__ float wave_min(float v) {
+#define Q3VL_DPPM(x, ctrl) \
+    __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), ctrl, 0xF, 0xF, false))
+    v = fminf(v, Q3VL_DPPM(v, 0xB1));
+    v = fminf(v, Q3VL_DPPM(v, 0x4E));
+    v = fminf(v, Q3VL_DPPM(v, 0x141));
+    v = fminf(v, Q3VL_DPPM(v, 0x140));
+#undef Q3VL_DPPM
+    return fminf(fminf(readlane_f(v, 0), readlane_f(v, 16)), fminf(readlane_f(v, 32), readlane_f(v, 48)));
+}
+
 // Left-to-right fold of the 8 lane accumulators held by lanes 0..7:
 // ((c0 + c1) + c2) + ... + c7; wave-uniform result.
 __device__ __forceinline__ float fold8_lanes(float c) {
@@ -428,10 +440,12 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_scores_kernel(
         float l = e;
 #pragma unroll
         for (int off = 32; off > 0; off >>= 1) l = l + __shfl_xor(l, off);
-        if (lane == 0) {
-            a.part_ml[((size_t)h * a.max_chunks + ch) * 2] = m;
-            a.part_ml[((size_t)h * a.max_chunks + ch) * 2 + 1] = l;
-        }
+        // the chunk's smallest score above -inf (+inf if none): the fold
+        // zeroes the head when exp256(min_c - M) is -inf, as the reference's
+        // softmax does when any of its terms is
+        const float mn = wave_min(lane < rows && score > -INFINITY ? score : INFINITY);
+        if (lane == 0)
+            *reinterpret_cast<float4 *>(a.part_ml + ((size_t)h * a.max_chunks + ch) * 4) = make_float4(m, l, mn, 0.0f);
     }
     }
     if constexpr (PAR) {
@@ -472,9 +486,14 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_scores_kernel(
 // c ascending:
 //   M = max_c m_c, w_c = exp256(m_c - M) (0 for m_c = -inf or M not finite),
 //   L = fma chain of w_c * l_c, O[d] = fma chain of w_c * o_c[d],
-//   out[d] = O[d] * (1.0f / L), or 0 where L is not finite and positive.
+//   out[d] = O[d] * (1.0f / L), or 0 where L is not finite and positive,
+//   and 0 for the whole head when M is finite and exp256(min_c - M) is -inf
+//   for some chunk (min_c its smallest score above -inf): then the
+//   reference's exp256(s_t - M) is -inf for that score (exp256 is -inf on a
+//   whole half-line and fl(s - M) is monotone in s), its sum is not finite
+//   and it zeroes the head (text_layer.cpp:512-515).
 // One block of 128 threads per query head. Every load is issued before the
-// values it feeds are needed: the (m_c, l_c) pairs of all chunks go to LDS
+// values it feeds are needed: the (m_c, l_c, min_c) of all chunks go to LDS
 // in one pass (one chunk per thread), the o_c[d] in batches of 16.
 constexpr int ATT_MAX_CHUNKS = 256;  // max_seq <= 16384
 __global__ __launch_bounds__(ATT_HD) void attn_combine_kernel(
@@ -486,14 +505,14 @@ __global__ __launch_bounds__(ATT_HD) void attn_combine_kernel(
     a.part_o = const_cast<float *>(part_o_p);
     a.max_chunks = max_chunks_p;
     a.max_seq = max_seq_p;
-    __shared__ float wsh[ATT_MAX_CHUNKS], lsh[ATT_MAX_CHUNKS], msh[ATT_MAX_CHUNKS];
+    __shared__ float wsh[ATT_MAX_CHUNKS], lsh[ATT_MAX_CHUNKS], msh[ATT_MAX_CHUNKS], nsh[ATT_MAX_CHUNKS];
     __shared__ float mred[2];
     const int h = blockIdx.x, d = threadIdx.x, lane = d & 63;
-    const float *ml = a.part_ml + (size_t)h * a.max_chunks * 2;
+    const float *ml = a.part_ml + (size_t)h * a.max_chunks * 4;
     const float *po = a.part_o + (size_t)h * a.max_chunks * ATT_HD + d;
     // the first chunks' partials go out before `pos` is known (indices
     // clamped into the buffers; chunks past the context are not used)
-    const float2 ml0 = *reinterpret_cast<const float2 *>(ml + 2 * min(d, a.max_chunks - 1));
+    const float4 ml0 = *reinterpret_cast<const float4 *>(ml + 4 * min(d, a.max_chunks - 1));
     float ob[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) ob[i] = po[(size_t)min(i, a.max_chunks - 1) * ATT_HD];
@@ -507,12 +526,14 @@ __global__ __launch_bounds__(ATT_HD) void attn_combine_kernel(
     if (d < nch) {
         msh[d] = ml0.x;
         lsh[d] = ml0.y;
+        nsh[d] = ml0.z;
         m = ml0.x;
     }
     for (int c = d + ATT_HD; c < nch; c += ATT_HD) {
-        const float2 v = *reinterpret_cast<const float2 *>(ml + 2 * c);
+        const float4 v = *reinterpret_cast<const float4 *>(ml + 4 * c);
         msh[c] = v.x;
         lsh[c] = v.y;
+        nsh[c] = v.z;
         m = fmaxf(m, v.x);
     }
     // M: the max of the m_c (a max is the same in any order: DPP moves
@@ -522,11 +543,16 @@ __global__ __launch_bounds__(ATT_HD) void attn_combine_kernel(
     __syncthreads();
     const float M = fmaxf(mred[0], mred[1]);
     const bool fin = __builtin_isfinite(M);
+    int vanish = 0;  // some score's exp256(s - M) is -inf
     for (int c = d; c < nch; c += ATT_HD) {
-        const float mc = msh[c];
+        const float mc = msh[c], mn = nsh[c];
         wsh[c] = (fin && mc > -INFINITY) ? exp256(mc - M) : 0.0f;
+        if (fin && mn < INFINITY && exp256(mn - M) == -INFINITY) vanish = 1;
     }
-    __syncthreads();
+    if (__syncthreads_or(vanish)) {
+        a.out[h * ATT_HD + d] = 0.0f;
+        return;
+    }
     float L = 0.0f, O = 0.0f;
     for (int c0 = 0; c0 < nch; c0 += 16) {
         float nb[16];
@@ -841,12 +867,17 @@ __global__ __launch_bounds__(PV_THREADS) void attn_softmax_pv_kernel(
 #pragma unroll
                 for (int u = 0; u < 16; ++u) V[u] = *reinterpret_cast<const float4 *>(vrow + tb + 4 * u);
             };
+            // a head whose sum is not finite and positive has invh = 0 (a
+            // finite positive sum is at most n, so its inverse is not 0):
+            // the reference zeroes its p (text_layer.cpp:512-515), and e * 0
+            // would be NaN for an e of -inf
+            const bool live = invh > 0.0f;
             auto run64 = [&](const float4 &E, const float4 *V, int tb) {
                 const int t = tb + 4 * rl;
-                const float p0 = t + 0 < len ? E.x * invh : 0.0f;
-                const float p1 = t + 1 < len ? E.y * invh : 0.0f;
-                const float p2 = t + 2 < len ? E.z * invh : 0.0f;
-                const float p3 = t + 3 < len ? E.w * invh : 0.0f;
+                const float p0 = live && t + 0 < len ? E.x * invh : 0.0f;
+                const float p1 = live && t + 1 < len ? E.y * invh : 0.0f;
+                const float p2 = live && t + 2 < len ? E.z * invh : 0.0f;
+                const float p3 = live && t + 3 < len ? E.w * invh : 0.0f;
                 asm volatile("s_nop 1" ::"v"(p0), "v"(p1), "v"(p2), "v"(p3));  // DPP read-after-write
 #pragma unroll
                 for (int k = 0; k < 16; ++k) fmac4_row_bcast(acc, p0, p1, p2, p3, V[k], k);

@@ -1602,6 +1602,21 @@ hipError_t launch_argmax_rows(const float *logits, int M, int V, float *pv, int3
     return launch_argmax_final(pv, pi, nparts, M, ids, st);
 }
 
+// n 32-bit words set to zero, as a kernel: a call captured into a HIP graph
+// then records a kernel node, not a memset node (memset nodes have given
+// wrong results on replays after the first on this platform).
+__global__ __launch_bounds__(256) void zero_words_kernel(uint32_t *p, size_t n) {
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) p[i] = 0u;
+}
+
+hipError_t launch_zero_words(void *p, size_t n, hipStream_t st) {
+    if (n == 0) return hipSuccess;
+    const size_t blocks = (n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096;
+    zero_words_kernel<<<(unsigned)blocks, 256, 0, st>>>(static_cast<uint32_t *>(p), n);
+    return hipGetLastError();
+}
+
 hipError_t launch_swiglu(float *gate, const float *up, size_t n, hipStream_t st) {
     if (n == 0) return hipSuccess;
     swiglu_kernel<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(gate, up, n);

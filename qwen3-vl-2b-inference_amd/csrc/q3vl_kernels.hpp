@@ -73,6 +73,8 @@ hipError_t launch_argmax_rows(const float *logits, int M, int V, float *part_val
                               hipStream_t st);
 // Stand-alone swiglu: gate[i] = silu(gate[i]) * up[i].
 hipError_t launch_swiglu(float *gate, const float *up, size_t n, hipStream_t st);
+// p[0..n) = 0 (32-bit words), by a kernel.
+hipError_t launch_zero_words(void *p, size_t n, hipStream_t st);
 
 // ------------------------------------------------------------ decode step
 struct AttnArgs {
@@ -83,7 +85,7 @@ struct AttnArgs {
     uint16_t *k_cache, *v_cache;            // fp16 [layers, kv_heads, max_seq, hd]
     const int32_t *pos;                     // device: position of the new token
     float *scores, *cmax;                   // scratch [heads, max_seq], [heads, max_chunks]
-    float *part_o, *part_ml;                // chunked order: [heads, max_chunks, hd], [heads, max_chunks, 2]
+    float *part_o, *part_ml;                // chunked order: [heads, max_chunks, hd], [heads, max_chunks, 4]: m, l, min, 0
     int order;                              // 0: the reference's order, 1: chunked
     float *out;                             // [heads*hd]
     int layer, heads, kv_heads, head_dim, max_seq, max_chunks, gs;

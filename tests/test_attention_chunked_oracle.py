@@ -10,8 +10,11 @@ the rest selects that value row exactly; a single chunk (at most 64
 positions) is its e-weighted values over its own sum. A score more than
 88.38 below the maximum makes exp256 return -inf (2^-128 is built as -inf),
 which zeroes the head in the reference order (text_layer.cpp:512-515): the
-chunked order gives zeros there too. A dropped chunk, a wrong chunk weight or
-a value row off by one position fails these.
+chunked order gives zeros there too, also when no chunk spans that gap by
+itself (a chunk at -50 and -100 against a maximum of 0 elsewhere: each factor
+exp256(-50) is finite, the reference's exp256(-100) is not), through each
+chunk's smallest finite score. A dropped chunk, a wrong chunk weight or a
+value row off by one position fails these.
 """
 import numpy as np
 import pytest
@@ -113,6 +116,38 @@ def test_score_gap_past_exp256_range_zeroes_the_head(orc, gap_chunk):
     for f in (orc.attention, orc.attention_chunked):
         got = f(q, kc, vc, H, KV, D, S, pos)
         np.testing.assert_array_equal(got, np.zeros_like(got))
+
+
+def scored(S, scores):
+    """q, k with score s_t = scores[t] for every head (dim 0 only)."""
+    q, kc, vc = case(11, S)
+    q[:] = 0.0
+    q[::D] = 1.0
+    kc[:, :, 0] = 0.0
+    kc[:, :len(scores), 0] = np.asarray(scores, np.float64) * np.sqrt(D)
+    return q, kc, vc
+
+
+@pytest.mark.parametrize("low,zero", [(-100.0, True), (-80.0, False)])
+def test_gap_spread_over_chunks(orc, low, zero):
+    """Chunk 1 (positions 64..127) has its maximum at -50 and its other
+    scores at `low`; chunks 0 and 2 are at 0, so M = 0. Within chunk 1 the
+    spread is 50 or 30 and against M the chunk factor is exp256(-50): all
+    finite. The reference order takes exp256(low - 0): -inf for -100 (the
+    head is zeroed), finite for -80 (the orders agree to exp256's error)."""
+    S, pos = 256, 150
+    s = np.zeros(pos + 1)
+    s[64:128] = low
+    s[90] = -50.0
+    q, kc, vc = scored(S, s)
+    ref = orc.attention(q, kc, vc, H, KV, D, S, pos)
+    got = orc.attention_chunked(q, kc, vc, H, KV, D, S, pos)
+    if zero:
+        np.testing.assert_array_equal(ref, np.zeros_like(ref))
+        np.testing.assert_array_equal(got, np.zeros_like(got))
+    else:
+        assert np.abs(ref).max() > 0.01
+        np.testing.assert_allclose(got, ref, rtol=0, atol=5e-4 * np.abs(ref).max())
 
 
 def test_all_scores_minus_infinity_gives_zeros(orc):

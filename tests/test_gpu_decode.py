@@ -26,10 +26,12 @@ def dev():
 class Stepper:
     """Device and oracle copies of one model + caches, stepped together."""
 
-    def __init__(self, dev, orc, dims, seed, ctx, token, stale_nan=False):
+    def __init__(self, dev, orc, dims, seed, ctx, token, stale_nan=False, qscale=1.0):
         torch, qm = dev
         self.torch, self.qm, self.orc, self.dims = torch, qm, orc, dims
         self.m = make_text_model(seed, dims)
+        if qscale != 1.0:  # larger queries through the q-norm's group scales
+            self.m["qnorm_s"] = (self.m["qnorm_s"] * np.float32(qscale)).astype(np.float32)
         k16, v16 = make_kv_cache(seed + 1, dims, ctx)
         if stale_nan:  # rows at and past ctx hold NaN bits, as an unwritten cache may
             k16[:, :, ctx:] = np.float16("nan")
@@ -200,6 +202,20 @@ def test_decode_chunked_full_config_step(dev, orc):
     s = Stepper(dev, orc, dims, seed=160, ctx=1024, token=151000)
     print("full-size chunked decode step: stepping", flush=True)
     s.step()
+
+
+@pytest.mark.parametrize("order", [0, CHUNKED])
+@pytest.mark.parametrize("qscale", [15.0, 100.0])
+def test_decode_wide_score_range(dev, orc, order, qscale):
+    """Queries scaled up by the q-norm's scales, so a head's scores (about
+    qscale * N(0, 1) against the N(0, 1) cache) spread past exp256's range:
+    at 15 over the context (~90) but mostly not within one 64-position chunk
+    (~70), at 100 within chunks too. The reference zeroes a head once some
+    exp256(s - M) is -inf (text_layer.cpp:512-515); both orders must zero
+    exactly those heads (the chunked order through each chunk's smallest
+    finite score), bit for bit against the oracle."""
+    dims = dict(SMALL, layers=1, max_seq=1088, attn_order=order)
+    Stepper(dev, orc, dims, seed=180, ctx=1000, token=9, qscale=qscale).step()
 
 
 def test_decode_chunked_position_out_of_range(dev):

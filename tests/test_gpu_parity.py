@@ -156,14 +156,34 @@ def test_gemm_group64_tiles_parity(orc, M, N, K):
 @pytest.mark.parametrize("M,N,K", [(100, 200, 1024), (333, 1030, 2048), (70, 300, 1536), (1030, 6200, 1024),
                                    (1030, 6200, 128)])
 def test_gemm_swiglu_ragged_parity(orc, M, N, K):
-    """SwiGLU GEMM: 64 x (64 + 64) tiles with 4-group w_s tiles (an odd
-    count at K = 1536), 128-row tiles once the grid outgrows one round of the
-    device (M = 1030), and the row-major kernel at K = 128."""
+    """SwiGLU GEMM: 64 x (64 + 64) tiles with 8-group w_s tiles (SG = 8;
+    an odd count, 3, at K = 1536), 128-row tiles once the grid outgrows one
+    round of the device (M = 1030), and the row-major kernel at K = 128."""
     A, Wg, Sg = make_case(900 + M, M, N, K, 64)
     _, Wu, Su = make_case(901 + M, M, N, K, 64)
     H = host(q.linear_i8_swiglu(dev(A), dev(Wg), dev(Sg), dev(Wu), dev(Su), 64))
     H_ref = orc.swiglu(orc.linear(A, Wg, Sg, 64), orc.linear(A, Wu, Su, 64))
     np.testing.assert_array_equal(H.view(np.uint32), H_ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("M,N", [(1, 1030), (3, 700), (40, 300)])
+def test_zero_k_gives_zeros(orc, M, N):
+    """K = 0: the reference's general path leaves C at zero and the argmax at
+    index 0 (the oracle agrees); the library writes them with its zero-fill
+    kernel over outputs that held NaN and 77."""
+    A = torch.empty((M, 0), dtype=torch.float32, device="cuda")
+    W = torch.empty((N, 0), dtype=torch.int8, device="cuda")
+    S = torch.empty((N, 0), dtype=torch.float32, device="cuda")
+    out = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
+    C = host(q.linear_i8(A, W, S, 64, out=out))
+    C_ref = orc.linear(np.zeros((M, 0), np.float32), np.zeros((N, 0), np.int8),
+                       np.zeros((N, 0), np.float32), 64)
+    assert_bits_equal(C, C_ref, f"K=0 {M}x{N}")
+    ids = torch.full((M,), 77, dtype=torch.int32, device="cuda")
+    logits = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
+    q.lm_head_argmax(A, W, S, 64, logits=logits, ids=ids)
+    np.testing.assert_array_equal(host(ids), orc.argmax_rows(C_ref))
+    assert_bits_equal(host(logits), C_ref, f"K=0 logits {M}x{N}")
 
 
 def test_golden_vectors_on_gpu():
