@@ -14,8 +14,9 @@ in a HIP graph and replayed; token and position live in device memory and
 each replay writes the next token and advances the position, so K steps
 generate K tokens at contexts 1024+W .. 1024+W+K-1. value = tokens/s.
 
-roofline: the dominant kernel of the decode step, gemv_kernel (every linear
-of the step and the lm_head; M=1 lane path), at the decode step's shapes:
+roofline: the dominant kernels of the decode step, its GEMVs
+(gemv_stream_kernel for q|k|v, o, gate|up and down, gemv_kernel for the
+lm_head; M=1 lane path), at the decode step's shapes:
 achieved = algorithmic bytes (int8 weights + fp32 group scales + fp32
 activations in and out) summed over one step's GEMV launches / the summed
 kernel durations, measured as HIP-graph replays of each class of launch
@@ -37,7 +38,9 @@ Also reported under "configs": config 0 (up_proj GEMV, GB/s), config 2
 (prefill gate|up+SwiGLU and down at M=512, TOPS), config 3 (lm_head GEMV +
 argmax, M=1 and 8, GB/s), config 4 (vision-encoder linears: 24 blocks of
 qkv/proj/fc1/fc2 at M=784 and the merger's fc1 and fc2 at M=196, TOPS), the
-exporter's weight quantizer on one up_proj ("export", GB/s) and, with
+exporter's weight quantizer on one up_proj ("export", GB/s), the C++
+linear() drop-in called with host pointers ("dropin": us per call at config
+0's shape, and tok/s over the 197 linears of a decode token) and, with
 --configs ...,load, the load of a full-size checkpoint file into HBM (GB/s of
 file bytes, page-cache-resident file).
 """
@@ -598,7 +601,8 @@ def decode_gemv_roofline(model, dims):
     step_bytes = sum(res[k]["bytes"] * n for k, n in per_step.items())
     launches = sum(per_step.values())
     gbs = step_bytes / (step_us * 1e-6) / 1e9
-    return dict(kernel="gemv_kernel<64, 1, true, R, KC, MD, P> (the decode step's GEMV launches)",
+    return dict(kernel="gemv_stream_kernel<KC, MD, R, NW> (q|k|v, o, gate|up, down) and "
+                       "gemv_kernel<64, 1, true, 8, 2048, MD, 1> (lm_head): the decode step's GEMV launches",
                 launches=launches,
                 bytes_per_launch=step_bytes / launches, avg_launch_us=step_us / launches,
                 achieved_GBs=gbs, frac=gbs / HBM_PEAK_GBS, step_gemv_us=step_us, by_class=res)
@@ -624,7 +628,27 @@ def bench_cfg0(args):
     return dict(name="cfg0_up_proj_gemv", metric="GB/s", value=gbs, ms=ms, eager_ms=eager_ms,
                 algo_bytes=algo, frac=gbs / HBM_PEAK_GBS, copies=n,
                 timing="HIP-graph replay of one launch per weight copy (eager_ms: per Python call)",
-                kernel="gemv_kernel<64, 1, true, 2, 2048, 0, 4>")
+                kernel="gemv_stream_kernel<2048, 0, 2, 8>")
+
+
+def bench_dropin(args):
+    """The engine's C++ linear() drop-in (matmul/include/hip_wrapper.hpp)
+    called as the reference engine calls its CPU linear(): host activations,
+    host weights (uploaded once by the weight registry), host output,
+    synchronous. q3vl_int8/linear_timing, a native program, times it (a
+    Python caller would add its own per-call cost): config 0's shape, and the
+    197 linears of one decode token (28 x q, k, v, o, gate, up, down, then
+    the lm_head) with every call's host work and waits. Child processes."""
+    exe = os.path.join(ROOT, "qwen3-vl-2b-inference_amd", "q3vl_int8", "linear_timing")
+    out = dict(name="dropin_linear", metric="us per call / tok/s",
+               timing="steady_clock around each linear() call, median; native caller")
+    for mode, arg in (("cfg0", "300"), ("seq", "5")):
+        r = subprocess.run([exe, mode, arg], capture_output=True, text=True, timeout=300)
+        if r.returncode != 0:
+            raise RuntimeError(f"linear_timing {mode}: rc {r.returncode}: {r.stderr[-500:]}")
+        out[mode] = json.loads(r.stdout.strip().splitlines()[-1])
+    out["value"] = out["seq"]["tok_s"]
+    return out
 
 
 def bench_cfg2(args):
@@ -882,7 +906,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200, help="timed decode steps (tokens)")
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--configs", default="cfg1,cfg1c,cfg0,cfg2,cfg3,cfg4,export")
+    ap.add_argument("--configs", default="cfg1,cfg1c,cfg0,cfg2,cfg3,cfg4,export,dropin")
     ap.add_argument("--cpu-budget", type=float, default=15.0,
                     help="seconds of reference CPU decode for cpu_baseline; the linear() "
                          "figures get a third of it each (0: skip the CPU leg)")
@@ -921,6 +945,7 @@ def main():
     results = []
     runners = {
         "cfg0": lambda: [bench_cfg0(args)],
+        "dropin": lambda: [bench_dropin(args)],
         "cfg2": lambda: [bench_cfg2(args)],
         "cfg3": lambda: [bench_cfg3(args, 1), bench_cfg3(args, 8)],
         "cfg4": lambda: [bench_cfg4(args)],
@@ -929,7 +954,7 @@ def main():
     }
     for c in configs:
         if c not in ("cfg1", "cfg1c") and c not in runners:
-            raise SystemExit(f"unknown config {c!r} (cfg0..cfg4, cfg1c, export, load)")
+            raise SystemExit(f"unknown config {c!r} (cfg0..cfg4, cfg1c, export, load, dropin)")
     decode_model = None
     for c in configs:
         log("bench:", c)

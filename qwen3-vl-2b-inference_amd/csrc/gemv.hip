@@ -1515,7 +1515,8 @@ static hipError_t launch_stream_md(const GemvArgs &a, const StreamCfg &c, int *g
 }
 
 // Whether the streaming kernel takes this lane-path launch: one activation
-// row, group 64, K of 2048 or 6144, plain or swiglu, no group-sum output.
+// row, group 64, K of 2048 or 6144, plain or swiglu, no group-sum output, at
+// most 16384 rows (the decode step's projections).
 // Q3VL_GEMV_STREAM=0 in the environment keeps every launch on gemv_kernel.
 static bool stream_takes(const GemvArgs &a) {
     static const bool enabled = [] {
@@ -1526,9 +1527,14 @@ static bool stream_takes(const GemvArgs &a) {
     if (a.mode != GEMV_PLAIN && a.mode != GEMV_SWIGLU) return false;
     if (a.mode == GEMV_SWIGLU && (a.nseg != 2 || a.K != 2048)) return false;
     if (a.norm_w && a.K != 2048) return false;
-    for (int s = 0; s < a.nseg; ++s)
+    int rows = 0;
+    for (int s = 0; s < a.nseg; ++s) {
         if (a.seg[s].G) return false;
-    return true;
+        rows += a.seg[s].N;
+    }
+    // (the lm_head's 151936 rows stay on gemv_kernel's 8-row tiles: 56
+    // against 64 us)
+    return rows <= 16384;
 }
 
 static hipError_t launch_stream(const GemvArgs &a, int *grid_out, hipStream_t st) {

@@ -10,7 +10,7 @@
 
 #include <cstdio>
 #include <cstdlib>
-#include <mutex>
+#include <cstring>
 
 #include "q3vl_int8.h"
 
@@ -32,21 +32,39 @@ bool is_device_ptr(const void *p) {
     exit(1);
 }
 
-// Grow-only device staging for host activations / outputs.
+// Grow-only staging for host activations and outputs, one set per calling
+// thread (no lock): pinned host buffers, so that the copies are asynchronous
+// DMA on the call's stream and the call waits once, and device buffers.
 struct Staging {
-    std::mutex mu;
-    void *a = nullptr;
-    size_t a_bytes = 0;
-    void *c = nullptr;
-    size_t c_bytes = 0;
-} g_stage;
+    void *ha = nullptr, *hc = nullptr;  // pinned host
+    size_t ha_bytes = 0, hc_bytes = 0;
+    void *da = nullptr, *dc = nullptr;  // device
+    size_t da_bytes = 0, dc_bytes = 0;
+    ~Staging() {
+        if (ha) (void)hipHostFree(ha);
+        if (hc) (void)hipHostFree(hc);
+        if (da) (void)hipFree(da);
+        if (dc) (void)hipFree(dc);
+    }
+};
+thread_local Staging t_stage;
 
-void *grow(void *&p, size_t &have, size_t need) {
+void *grow_device(void *&p, size_t &have, size_t need) {
     if (need <= have) return p;
     if (p) (void)hipFree(p);
     p = nullptr;
     have = 0;
     if (hipMalloc(&p, need) != hipSuccess) die("staging hipMalloc failed");
+    have = need;
+    return p;
+}
+
+void *grow_pinned(void *&p, size_t &have, size_t need) {
+    if (need <= have) return p;
+    if (p) (void)hipHostFree(p);
+    p = nullptr;
+    have = 0;
+    if (hipHostMalloc(&p, need, hipHostMallocDefault) != hipSuccess) die("staging hipHostMalloc failed");
     have = need;
     return p;
 }
@@ -86,24 +104,42 @@ void linear(const void *mat_A, const void *mat_B_in, const void *mat_B_scale,
             die(q3vl_last_error());
     }
 
-    std::lock_guard<std::mutex> lk(g_stage.mu);
+    // Host activations and outputs go through this thread's pinned staging:
+    // upload, kernel and download are queued on the null stream (ordered
+    // after the engine's own device work, as the synchronous copies were) and
+    // the call waits once.
+    Staging &st = t_stage;
+    const size_t a_bytes = M * K * sizeof(float), c_bytes = M * N * sizeof(float);
     const float *dA = static_cast<const float *>(mat_A);
     if (!is_device_ptr(mat_A)) {
-        void *p = grow(g_stage.a, g_stage.a_bytes, M * K * sizeof(float) + 16);
-        if (hipMemcpy(p, mat_A, M * K * sizeof(float), hipMemcpyHostToDevice) != hipSuccess)
+        void *h = grow_pinned(st.ha, st.ha_bytes, a_bytes);
+        void *d = grow_device(st.da, st.da_bytes, a_bytes + 16);
+        memcpy(h, mat_A, a_bytes);
+        if (hipMemcpyAsync(d, h, a_bytes, hipMemcpyHostToDevice, nullptr) != hipSuccess)
             die("activation upload failed");
-        dA = static_cast<const float *>(p);
+        dA = static_cast<const float *>(d);
     }
+    // A host C of a GEMV (M <= 8: at most 8 rows) is written by the kernel
+    // straight into the pinned buffer (device-accessible host memory), with
+    // no download; a larger one goes through a device buffer and a copy.
     const bool c_host = !is_device_ptr(mat_C);
+    const bool c_direct = c_host && M <= 8;
     float *dC = static_cast<float *>(mat_C);
-    if (c_host) dC = static_cast<float *>(grow(g_stage.c, g_stage.c_bytes, M * N * sizeof(float)));
+    void *hc = nullptr;
+    if (c_host) hc = grow_pinned(st.hc, st.hc_bytes, c_bytes);
+    if (c_direct) {
+        void *p = nullptr;
+        if (hipHostGetDevicePointer(&p, hc, 0) != hipSuccess) die("hipHostGetDevicePointer failed");
+        dC = static_cast<float *>(p);
+    } else if (c_host) {
+        dC = static_cast<float *>(grow_device(st.dc, st.dc_bytes, c_bytes));
+    }
 
     if (q3vl_linear_i8(dA, dW, dS, dC, M, N, K, group_size, nullptr, 0, nullptr) != Q3VL_OK)
         die(q3vl_last_error());
-    if (c_host) {
-        if (hipMemcpy(mat_C, dC, M * N * sizeof(float), hipMemcpyDeviceToHost) != hipSuccess)
-            die("result download failed");
-    } else if (hipStreamSynchronize(nullptr) != hipSuccess) {
-        die("hipStreamSynchronize failed");
-    }
+    if (c_host && !c_direct &&
+        hipMemcpyAsync(hc, dC, c_bytes, hipMemcpyDeviceToHost, nullptr) != hipSuccess)
+        die("result download failed");
+    if (hipStreamSynchronize(nullptr) != hipSuccess) die("hipStreamSynchronize failed");
+    if (c_host) memcpy(mat_C, hc, c_bytes);
 }
