@@ -844,6 +844,155 @@ def pmc_workload():
     log("pmc workload done")
 
 
+def pmc_workload_gemm():
+    """Workload for the GEMM counter passes: 4 eager calls of each of config
+    2's GEMMs (gate|up with the SwiGLU epilogue, then down, M = 512) and of
+    config 4's vision linears (qkv, proj, fc1, fc2 at M = 784; the merger's
+    fc1 at M = 196), each call its fragment-order quantizer and its
+    gemm_mf_kernel."""
+    import torch
+    import q3vl_int8 as q
+    shapes = [("cfg2 gate|up", 512, 6144, 2048, True), ("cfg2 down", 512, 2048, 6144, False)]
+    shapes += [(f"cfg4 {n}", VIS_T, N, K, False) for n, (N, K) in zip(("qkv", "proj", "fc1", "fc2"), VIS_SHAPES)]
+    shapes += [("cfg4 merger fc1", VIS_T // 4, MERGER_SHAPES[0][0], MERGER_SHAPES[0][1], False)]
+    for name, M, N, K, sw in shapes:
+        W, S = gen_weights(N, K, 1, 11)
+        A = torch.randn((M, K), dtype=torch.float32, device="cuda")
+        out = torch.empty((M, N), dtype=torch.float32, device="cuda")
+        ws = q.alloc_workspace(M, N, K, GS)
+        for _ in range(4):
+            if sw:
+                W2, S2 = gen_weights(N, K, 1, 12)
+                q.linear_i8_swiglu(A, W[0], S[0], W2[0], S2[0], GS, out=out, workspace=ws)
+            else:
+                q.linear_i8(A, W[0], S[0], GS, out=out, workspace=ws)
+        torch.cuda.synchronize()
+        log(f"pmc gemm workload: {name} {M}x{N}x{K} done")
+
+
+def pmc_summary(dirs, match):
+    """Average counter values per dispatch for the kernels whose name holds
+    `match`, from rocprofv3 --pmc runs (counter_collection.csv under each
+    directory; one run per pass), grouped by kernel name and grid size, with
+    the derived figures:
+      active_cycles = GRBM_GUI_ACTIVE / 8 (the GRBM count is summed over the
+                      8 XCDs: the kernel's own busy cycles on each),
+      mfma_busy  = SQ_VALU_MFMA_BUSY_CYCLES / (1024 SIMDs * active_cycles),
+      valu_busy  = 4 * SQ_ACTIVE_INST_VALU / (1024 * active_cycles)
+                   (SQ_ACTIVE_INST_VALU counts quad-cycles),
+      lds_bank_conflict = SQ_LDS_BANK_CONFLICT / SQ_ACTIVE_INST_LDS (bank-
+                   conflict cycles per LDS-active cycle),
+      waves_per_simd = SQ_WAVE_CYCLES / SQ_BUSY_CYCLES / 4,
+      valu_per_mfma = SQ_INSTS_VALU / SQ_INSTS_MFMA."""
+    import csv
+    import glob
+    vals = {}
+    for d in dirs:
+        for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            with open(f, newline="") as fh:
+                for r in csv.DictReader(fh):
+                    name = r.get("Kernel_Name", "")
+                    if match not in name:
+                        continue
+                    key = f"{name} [grid {r.get('Grid_Size', r.get('Grid_Size_X', '?'))}]"
+                    vals.setdefault(key, {}).setdefault(r["Counter_Name"], []).append(float(r["Counter_Value"]))
+    simds, xcds = 1024, 8
+    out = {}
+    for key, cs in sorted(vals.items()):
+        avg = {c: sum(v) / len(v) for c, v in cs.items()}
+        e = dict(dispatches={c: len(v) for c, v in cs.items()}, avg_per_dispatch={c: round(v, 1) for c, v in avg.items()})
+        g = avg.get("GRBM_GUI_ACTIVE")
+        derived = {}
+        if g:
+            derived["active_cycles"] = round(g / xcds)
+        if g and "SQ_VALU_MFMA_BUSY_CYCLES" in avg:
+            derived["mfma_busy"] = round(avg["SQ_VALU_MFMA_BUSY_CYCLES"] / (simds * g / xcds), 4)
+        if g and "SQ_ACTIVE_INST_VALU" in avg:
+            derived["valu_busy"] = round(4 * avg["SQ_ACTIVE_INST_VALU"] / (simds * g / xcds), 4)
+        if avg.get("SQ_ACTIVE_INST_LDS") and "SQ_LDS_BANK_CONFLICT" in avg:
+            derived["lds_bank_conflict"] = round(avg["SQ_LDS_BANK_CONFLICT"] / avg["SQ_ACTIVE_INST_LDS"], 4)
+        if avg.get("SQ_BUSY_CYCLES") and "SQ_WAVE_CYCLES" in avg:
+            derived["waves_per_simd"] = round(avg["SQ_WAVE_CYCLES"] / avg["SQ_BUSY_CYCLES"] / 4, 3)
+        if "SQ_INSTS_VALU" in avg and avg.get("SQ_INSTS_MFMA"):
+            derived["valu_per_mfma"] = round(avg["SQ_INSTS_VALU"] / avg["SQ_INSTS_MFMA"], 3)
+        e["derived"] = derived
+        out[key] = e
+    return out
+
+
+def pmc_traffic(fetch_dir, write_dir):
+    """HBM bytes per decode GEMV launch from two rocprofv3 --pmc runs of
+    `--pmc-workload` (FETCH_SIZE, then WRITE_SIZE; KiB per dispatch), each
+    scaled by what the same counter reads for the workload's calibration copy
+    (dst = src + 1 over 256 MiB of uint8: 256 MiB read, 256 MiB written)."""
+    import csv
+    import glob
+
+    def per_kernel(d, counter):
+        rows = {}
+        for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            with open(f, newline="") as fh:
+                for r in csv.DictReader(fh):
+                    if r["Counter_Name"] == counter:
+                        rows.setdefault(r.get("Kernel_Name", ""), []).append(float(r["Counter_Value"]))
+        return rows
+
+    fetch, write = per_kernel(fetch_dir, "FETCH_SIZE"), per_kernel(write_dir, "WRITE_SIZE")
+    # the calibration copy: the elementwise dispatch that reads the most
+    # (torch's fills of the workload's buffers are elementwise too)
+    cands = [(max(v), k) for k, v in fetch.items() if "elementwise" in k]
+    if not cands:
+        raise SystemExit("no calibration (elementwise) dispatch in the FETCH_SIZE run")
+    cal = [max(cands)[1]]
+    n_cal = 256 << 20
+    f_cal = max(fetch[cal[0]])
+    w_cal = max(max(v) for k, v in write.items() if "elementwise" in k)
+    ff, wf = n_cal / (f_cal * 1024), n_cal / (w_cal * 1024)
+    gemv = [k for k in fetch if "gemv" in k]
+    nd = sum(len(fetch[k]) for k in gemv)
+    fk = sum(sum(fetch[k]) for k in gemv) / nd
+    wk = sum(sum(write.get(k, [0.0])) for k in gemv) / nd
+    hbm = fk * 1024 * ff + wk * 1024 * wf
+    # algorithmic bytes per launch, as decode_gemv_roofline counts them
+    # (weights, scales, activations in and out; SwiGLU writes one output)
+    dims = decode_dims(max_seq=CTX + 16)
+    per_layer, head = decode_gemv_shapes(dims)
+    tot = 0
+    for name, segs in per_layer:
+        K = segs[0][1]
+        tot += (sum(wbytes(N, K) for N, _ in segs) + K * 4 +
+                (segs[0][0] if name == "gate_up" else sum(N for N, _ in segs)) * 4) * dims["layers"]
+    tot += wbytes(*head[1][0]) + head[1][0][1] * 4 + head[1][0][0] * 4
+    algo = round(tot / (4 * dims["layers"] + 1))
+    return {
+        "kernel": "the decode step's GEMVs: q3vl::gemv_stream_kernel<KC, MD, R, NW> (q|k|v, o, "
+                  "gate|up, down) and q3vl::gemv_kernel<64, 1, true, 8, 2048, 2, 1> (lm_head)",
+        "workload": "3 eager decode steps of config 1 (113 GEMV launches each: q|k|v, o, gate|up, "
+                    "down x 28 layers, lm_head)",
+        "dispatches": nd,
+        "dispatches_by_variant": {k: len(fetch[k]) for k in sorted(gemv)},
+        "fetch_size_kib_per_dispatch": round(fk, 1),
+        "write_size_kib_per_dispatch": round(wk, 1),
+        "calibration": {"kernel": "dst = src + 1 over 256 MiB uint8 (torch elementwise add)",
+                        "bytes_read": n_cal, "bytes_written": n_cal,
+                        "fetch_size_kib": f_cal, "write_size_kib": w_cal,
+                        "fetch_factor": round(ff, 4), "write_factor": round(wf, 4)},
+        "hbm_bytes_per_launch": round(hbm),
+        "algorithmic_bytes_per_launch": algo,
+        "traffic_over_algorithmic": round(hbm / algo, 4),
+        "commands": [
+            "cd /tmp && TMPDIR=/tmp rocprofv3 --pmc FETCH_SIZE --output-format csv -d "
+            "$ROOT/gpurun_out/<fetch_dir> -o run -- python3 $ROOT/bench.py --pmc-workload",
+            "cd /tmp && TMPDIR=/tmp rocprofv3 --pmc WRITE_SIZE --output-format csv -d "
+            "$ROOT/gpurun_out/<write_dir> -o run -- python3 $ROOT/bench.py --pmc-workload",
+            "python3 bench.py --pmc-traffic <fetch_dir> <write_dir>"],
+        "other_kernels_same_run": {
+            k: {"fetch_kib": round(sum(v) / len(v), 1),
+                "write_kib": round(sum(write.get(k, [0.0])) / max(1, len(write.get(k, []))), 1)}
+            for k, v in sorted(fetch.items()) if k not in gemv and "elementwise" not in k},
+    }
+
+
 def load_traffic():
     """HBM bytes per gemv_kernel launch from the committed counter summary
     (FETCH_SIZE + WRITE_SIZE per dispatch, scaled by the copy calibration)."""
@@ -915,13 +1064,27 @@ def main():
     ap.add_argument("--cpu-timeout", type=float, default=300.0)
     ap.add_argument("--cpu-leg", action="store_true",
                     help="(internal) run only the reference CPU leg and print its JSON")
-    ap.add_argument("--pmc-workload", action="store_true",
-                    help="run only the workload of the HBM-traffic counter passes")
+    ap.add_argument("--pmc-summary", nargs="+", metavar="DIR",
+                    help="print per-dispatch counter averages (and derived GEMM figures) of the "
+                         "kernels named by --pmc-match from rocprofv3 --pmc output directories")
+    ap.add_argument("--pmc-match", default="gemm_mf_kernel")
+    ap.add_argument("--pmc-traffic", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="print the decode GEMVs' HBM traffic summary from the FETCH_SIZE and "
+                         "WRITE_SIZE runs of --pmc-workload")
+    ap.add_argument("--pmc-workload", nargs="?", const="decode", choices=["decode", "gemm"],
+                    help="run only the workload of the counter passes: decode (the decode "
+                         "GEMVs' HBM traffic, the default) or gemm (configs 2 and 4's GEMMs)")
     ap.add_argument("--trace-summary", metavar="KERNEL_TRACE_CSV",
                     help="summarize a rocprofv3 kernel trace of this bench and exit")
     args = ap.parse_args()
     if args.trace_summary:
         print(json.dumps(trace_summary(args.trace_summary), indent=1))
+        return
+    if args.pmc_summary:
+        print(json.dumps(pmc_summary(args.pmc_summary, args.pmc_match), indent=1))
+        return
+    if args.pmc_traffic:
+        print(json.dumps(pmc_traffic(*args.pmc_traffic), indent=1))
         return
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (see the sharding "
@@ -938,7 +1101,7 @@ def main():
     q.lib()  # fails loudly if the HIP library is missing
     torch.cuda.set_device(0)
     if args.pmc_workload:
-        pmc_workload()
+        pmc_workload_gemm() if args.pmc_workload == "gemm" else pmc_workload()
         return
     configs = args.configs.split(",")
     dims = decode_dims(max_seq=(CTX + args.warmup + args.steps + 7 + 15) // 8 * 8)
