@@ -880,8 +880,8 @@ def pmc_summary(dirs, match):
       mfma_busy  = SQ_VALU_MFMA_BUSY_CYCLES / (1024 SIMDs * active_cycles),
       valu_busy  = 4 * SQ_ACTIVE_INST_VALU / (1024 * active_cycles)
                    (SQ_ACTIVE_INST_VALU counts quad-cycles),
-      lds_bank_conflict = SQ_LDS_BANK_CONFLICT / SQ_ACTIVE_INST_LDS (bank-
-                   conflict cycles per LDS-active cycle),
+      lds_conflict_per_instr = SQ_LDS_BANK_CONFLICT / SQ_INSTS_LDS (stall
+                   cycles from LDS bank conflicts per LDS instruction),
       waves_per_simd = SQ_WAVE_CYCLES / SQ_BUSY_CYCLES / 4,
       valu_per_mfma = SQ_INSTS_VALU / SQ_INSTS_MFMA."""
     import csv
@@ -909,8 +909,8 @@ def pmc_summary(dirs, match):
             derived["mfma_busy"] = round(avg["SQ_VALU_MFMA_BUSY_CYCLES"] / (simds * g / xcds), 4)
         if g and "SQ_ACTIVE_INST_VALU" in avg:
             derived["valu_busy"] = round(4 * avg["SQ_ACTIVE_INST_VALU"] / (simds * g / xcds), 4)
-        if avg.get("SQ_ACTIVE_INST_LDS") and "SQ_LDS_BANK_CONFLICT" in avg:
-            derived["lds_bank_conflict"] = round(avg["SQ_LDS_BANK_CONFLICT"] / avg["SQ_ACTIVE_INST_LDS"], 4)
+        if avg.get("SQ_INSTS_LDS") and "SQ_LDS_BANK_CONFLICT" in avg:
+            derived["lds_conflict_per_instr"] = round(avg["SQ_LDS_BANK_CONFLICT"] / avg["SQ_INSTS_LDS"], 3)
         if avg.get("SQ_BUSY_CYCLES") and "SQ_WAVE_CYCLES" in avg:
             derived["waves_per_simd"] = round(avg["SQ_WAVE_CYCLES"] / avg["SQ_BUSY_CYCLES"] / 4, 3)
         if "SQ_INSTS_VALU" in avg and avg.get("SQ_INSTS_MFMA"):
