@@ -659,24 +659,23 @@ def bench_cfg2(args):
     Wu, Su = gen_weights(I, K, 1, 2)
     Wd, Sd = gen_weights(K, I, 1, 3)
     A = torch.randn((M, K), dtype=torch.float32, device="cuda")
-    H = torch.empty((M, I), dtype=torch.float32, device="cuda")
     D = torch.empty((M, K), dtype=torch.float32, device="cuda")
-    ws = q.alloc_workspace(M, I, max(K, I), GS)
+    ws = torch.zeros(q.mlp_workspace_bytes(M, K, I, GS), dtype=torch.uint8, device="cuda")
 
-    def step():
-        q.linear_i8_swiglu(A, Wg[0], Sg[0], Wu[0], Su[0], GS, out=H, workspace=ws)
-        q.linear_i8(H, Wd[0], Sd[0], GS, out=D, workspace=ws)
+    def step():  # the MLP block: gate|up + SwiGLU, then down (q3vl_mlp_i8)
+        q.mlp_i8(A, Wg[0], Sg[0], Wu[0], Su[0], Wd[0], Sd[0], GS, out=D, workspace=ws)
 
-    # one HIP graph of the step (two quantizers and two GEMMs), replayed: the
-    # kernels back to back, without the host time of eager Python calls
+    # one HIP graph of the step, replayed: the kernels back to back, without
+    # the host time of eager Python calls
     ms = _graph_time([step], reps=10, region="cfg2")
     ops = cfg2_ops(M, K, I)
     tops = ops / (ms * 1e-3) / 1e12
     return dict(name="cfg2_prefill_gemm", metric="TOPS", value=tops, ms=ms, algo_ops=ops,
                 frac=tops / FP16_PEAK_TFLOPS, frac_of_int8_peak=tops / INT8_PEAK_TOPS,
-                timing="HIP-graph replay of the step (quantizers and GEMMs)",
+                timing="HIP-graph replay of the MLP block (q3vl_mlp_i8: A's quantizer and "
+                       "the two GEMMs)",
                 kernel="quantize_frag_kernel + gemm_mf_kernel: gate|up with the SwiGLU "
-                       "epilogue, then down")
+                       "epilogue quantizing h into down's operand, then down")
 
 
 def bench_cfg3(args, M):

@@ -132,6 +132,22 @@ int q3vl_linear_i8_swiglu(const float *A, const int8_t *Wg, const float *Sg,
                           void *workspace, size_t workspace_bytes,
                           q3vl_stream stream);
 
+/* The MLP block of forward_text (model/src/forward.cpp:619-654): the gate
+ * and up linear() calls, swiglu (layers/src/text_layer.cpp:420-434) and the
+ * down linear() call: Y = (silu(A Wg^T) * (A Wu^T)) Wd^T with A [M,H],
+ * Wg/Wu [I,H], Wd [H,I], Y [M,H]; the numerics of those four calls (the down
+ * projection quantizes h as the reference's linear() quantizes state->gate).
+ * With M > 8, group size 64 and H, I multiples of 512, the gate|up GEMM's
+ * epilogue quantizes h straight into the down GEMM's operand (no h in
+ * memory, one quantizer launch fewer); otherwise the two calls run through
+ * an h buffer in the workspace (>= q3vl_mlp_workspace_bytes()). */
+int q3vl_mlp_i8(const float *A, const int8_t *Wg, const float *Sg,
+                const int8_t *Wu, const float *Su, const int8_t *Wd,
+                const float *Sd, float *Y, size_t M, size_t H, size_t I,
+                size_t group_size, void *workspace, size_t workspace_bytes,
+                q3vl_stream stream);
+size_t q3vl_mlp_workspace_bytes(size_t M, size_t H, size_t I, size_t group_size);
+
 /* lm_head (classifier_gemm, layers/src/text_layer.cpp:302-314) fused with
  * greedy_decode (tokenizer/src/utils.cpp:34-44): ids[m] = first index of the
  * maximum of row m of A W^T (W [V,K]). logits may be NULL (not stored) for

@@ -593,6 +593,99 @@ int q3vl_linear_i8_swiglu(const float *A, const int8_t *Wg, const float *Sg, con
                       workspace_bytes, (hipStream_t)stream, nullptr);
 }
 
+// The MLP block: h = swiglu(A Wg^T, A Wu^T) [M, I], then Y = h Wd^T [M, H].
+// Fused where the fragment-order GEMMs serve both products: A quantized
+// once, the gate|up GEMM's epilogue quantizes h into the down GEMM's operand
+// (no h in memory, no quantizer launch for it). Elsewhere: the two calls
+// through an h buffer at the start of the workspace.
+struct MlpLayout {
+    bool fused = false;
+    size_t aq = 0, as = 0, hq = 0, hs = 0;  // fused
+    size_t h = 0, inner = 0;                // two calls: h, then the calls' own workspace
+    size_t total = 0;
+};
+
+static MlpLayout mlp_layout(size_t M, size_t H, size_t I, size_t gs, bool fused) {
+    MlpLayout L;
+    L.fused = fused;
+    size_t off = 0;
+    if (fused) {
+        const size_t Mpad = (M + 31) & ~(size_t)31;
+        L.aq = off;
+        off += align256(Mpad * H * 2);
+        L.as = off;
+        off += align256(Mpad * (H / 64) * 4);
+        L.hq = off;
+        off += align256(Mpad * I * 2);
+        L.hs = off;
+        off += align256(Mpad * (I / 64) * 4);
+    } else {
+        L.h = off;
+        off += align256(M * I * 4);
+        L.inner = off;
+        const size_t a = q3vl_workspace_bytes(M, I, H, gs), b = q3vl_workspace_bytes(M, H, I, gs);
+        off += a > b ? a : b;
+    }
+    L.total = off;
+    return L;
+}
+
+static bool mlp_fuses(size_t M, size_t H, size_t I, size_t gs, int cus) {
+    const size_t Mpad = (M + 31) & ~(size_t)31;
+    return M > 8 && gs == 64 && H % 512 == 0 && I % 512 == 0 && Mpad * (H > I ? H : I) * 2 <= 0x7fffffffULL &&
+           H * I <= 0x7fffffffULL && gemm_mf_serves((int)M, (int)I, (int)H, true, cus) &&
+           gemm_mf_serves((int)M, (int)H, (int)I, false, cus);
+}
+
+size_t q3vl_mlp_workspace_bytes(size_t M, size_t H, size_t I, size_t group_size) {
+    const size_t a = mlp_layout(M, H, I, group_size ? group_size : 1, false).total;
+    const size_t b = (group_size == 64 && H % 512 == 0 && I % 512 == 0 && M > 8)
+                         ? mlp_layout(M, H, I, 64, true).total : 0;
+    return a > b ? a : b;
+}
+
+int q3vl_mlp_i8(const float *A, const int8_t *Wg, const float *Sg, const int8_t *Wu, const float *Su,
+                const int8_t *Wd, const float *Sd, float *Y, size_t M, size_t H, size_t I,
+                size_t group_size, void *workspace, size_t workspace_bytes, q3vl_stream stream) {
+    const hipStream_t st = (hipStream_t)stream;
+    if (!Y && M && H) return fail(Q3VL_ERR_INVALID_ARGUMENT, "null Y");
+    int rc = check_common(A, Wg, Sg, M, I, H, group_size);
+    if (!rc) rc = check_common(A, Wu, Su, M, I, H, group_size);
+    if (!rc) rc = check_common(A, Wd, Sd, M, H, I, group_size);
+    if (rc) return rc;
+    if (M == 0 || H == 0) return Q3VL_OK;
+    int cus = 0;
+    rc = device_cus(&cus);
+    if (rc) return rc;
+    const bool fused = I > 0 && mlp_fuses(M, H, I, group_size, cus);
+    const MlpLayout L = mlp_layout(M, H, I, group_size, fused);
+    char *wbase = nullptr;
+    rc = resolve_ws(workspace, workspace_bytes, L.total, &wbase);
+    if (rc) return rc;
+    if (fused) {
+        _Float16 *aq = reinterpret_cast<_Float16 *>(wbase + L.aq);
+        float *as = reinterpret_cast<float *>(wbase + L.as);
+        _Float16 *hq = reinterpret_cast<_Float16 *>(wbase + L.hq);
+        float *hs = reinterpret_cast<float *>(wbase + L.hs);
+        const int Mt = (int)((M + 31) / 32);
+        Q3VL_HIP(launch_quantize_frag(A, aq, as, (int)M, (int)H, st), "quantize launch");
+        GemmMfArgs gu{aq, as, Mt, Wg, Sg, Wu, Su, nullptr, (int)M, (int)I, (int)H};
+        gu.hq = hq;
+        gu.hqs = hs;
+        Q3VL_HIP(launch_gemm_mf(gu, true, cus, st), "gate|up gemm launch");
+        GemmMfArgs dn{hq, hs, Mt, Wd, Sd, nullptr, nullptr, Y, (int)M, (int)H, (int)I};
+        Q3VL_HIP(launch_gemm_mf(dn, false, cus, st), "down gemm launch");
+        return Q3VL_OK;
+    }
+    // the two calls, h in the workspace
+    float *h = reinterpret_cast<float *>(wbase + L.h);
+    char *inner = wbase + L.inner;
+    const size_t inner_bytes = L.total - L.inner;
+    rc = q3vl_linear_i8_swiglu(A, Wg, Sg, Wu, Su, h, M, I, H, group_size, inner, inner_bytes, stream);
+    if (rc) return rc;
+    return q3vl_linear_i8(h, Wd, Sd, Y, M, H, I, group_size, inner, inner_bytes, stream);
+}
+
 int q3vl_lm_head_argmax(const float *A, const int8_t *W, const float *S, float *logits,
                         int32_t *ids, size_t M, size_t V, size_t K, size_t group_size,
                         void *workspace, size_t workspace_bytes, q3vl_stream stream) {

@@ -171,7 +171,10 @@ __device__ __forceinline__ int bslot(int s, int l) {
 // return turns into a wait for the whole ring. SG: groups per w_s tile (a
 // power of two, at most kWsTile; K must be a multiple of 64 kWsTile).
 constexpr int kWsTile = 8;
-template <int TM, int TN, bool SWIGLU, int D, int BPC, int WM = 2, bool AL = true, int SG = kWsTile>
+// HQ (SwiGLU only): the epilogue quantizes h into the down GEMM's operand
+// (GemmMfArgs::hq) instead of storing it.
+template <int TM, int TN, bool SWIGLU, int D, int BPC, int WM = 2, bool AL = true, int SG = kWsTile,
+          bool HQ = false>
 // What the entry loads need comes first, as plain arguments that the
 // dispatcher preloads into scalar registers (the up scales and the rest are
 // read from the GemmMfArgs copy).
@@ -566,6 +569,92 @@ __global__ __launch_bounds__(256, BPC) void gemm_mf_kernel(
         }
     }
 
+    // ---- SwiGLU with hq: the block's h tile (MTB m-tiles x 64 columns, one
+    // whole group of the down projection's K) quantized straight into the
+    // down GEMM's fragment-order operand, with quantize_frag_kernel's layout
+    // and numerics (i8:135-177: the 16 chains over elements 16t + c, V[i] =
+    // P[i] + P[i+8], the fixed tree, s = rms * fp32(1/127), RNE(h / s)), in
+    // place of storing h: a quad of lanes per (row, group), lane u holding
+    // elements 16t + 4u .. 4u + 3 (chains 4u .. 4u + 3). Rows past M get q = 0
+    // and a_s = 0, as the quantizer's padding rows do.
+    if constexpr (SWIGLU && HQ) {
+        {
+            constexpr int HLD = 68;  // floats per h row in LDS (64 + 4)
+            float *ht = reinterpret_cast<float *>(smem);  // (the last group's barrier has passed)
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int rr = 32 * (wm * TM + i) + 4 * h + 8 * (e >> 2) + (e & 3);
+                    ht[rr * HLD + 32 * wn + (lane & 31)] = silu_mul(out[i][0][e], out[i][1][e]);
+                }
+            lds_barrier();
+            const int Kgo = N / 64, go = n0 / 64;
+            // (the thread index is rebuilt from mbcnt here rather than kept
+            // live across the K loop, where one more VGPR spills per group)
+            const int lid = (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+#pragma unroll
+            for (int p = 0; p < MTB * 128 / 256; ++p) {
+                const int idx = 64 * wid + lid + 256 * p, rr = idx >> 2, u = idx & 3;
+                const int mt = mt0 + (rr >> 5), r = rr & 31;
+                const bool real = 32 * mt + r < M;  // the same for the quad
+                float4 cv[4];
+#pragma unroll
+                for (int t = 0; t < 4; ++t)
+                    cv[t] = real ? *reinterpret_cast<const float4 *>(ht + rr * HLD + 16 * t + 4 * u)
+                                 : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                float p0 = 0.0f, p1 = 0.0f, p2 = 0.0f, p3 = 0.0f;
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    p0 = fmaf(cv[t].x, cv[t].x, p0);
+                    p1 = fmaf(cv[t].y, cv[t].y, p1);
+                    p2 = fmaf(cv[t].z, cv[t].z, p2);
+                    p3 = fmaf(cv[t].w, cv[t].w, p3);
+                }
+#define Q3VL_QUAD(v, ctrl) \
+    __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), ctrl, 0xF, 0xF, false))
+                // lanes 0, 1 take lanes 2, 3 (quad_perm [2,3,2,3]); lane 0 takes
+                // lane 1's V[4..7] ([1,1,1,1]); lane 0's sum to the quad ([0,0,0,0])
+                const float v0 = p0 + Q3VL_QUAD(p0, 0xEE), v1 = p1 + Q3VL_QUAD(p1, 0xEE);
+                const float v2 = p2 + Q3VL_QUAD(p2, 0xEE), v3 = p3 + Q3VL_QUAD(p3, 0xEE);
+                const float w0 = Q3VL_QUAD(v0, 0x55), w1 = Q3VL_QUAD(v1, 0x55);
+                const float w2 = Q3VL_QUAD(v2, 0x55), w3 = Q3VL_QUAD(v3, 0x55);
+                const float sumsq = Q3VL_QUAD(tree8(v0, v1, v2, v3, w0, w1, w2, w3), 0x00);
+#undef Q3VL_QUAD
+                const float sc = group_scale(sumsq, 1.0f / 64.0f);
+                const float inv = rcp_rn(sc);
+                if (mt < Mt) {  // (a block's last m-tile may lie past the product)
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        uint32_t q0 = quant_pair_finite(cv[t].x * inv, cv[t].y * inv);
+                        uint32_t q1 = quant_pair_finite(cv[t].z * inv, cv[t].w * inv);
+                        if (__builtin_expect(!__builtin_isfinite(sc), 0)) {
+                            q0 = quant_pair(cv[t].x * inv, cv[t].y * inv);
+                            q1 = quant_pair(cv[t].z * inv, cv[t].w * inv);
+                        }
+                        const uint32_t h0 = real ? __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(
+                                                       (float)(int16_t)(q0 & 0xFFFF), (float)(int16_t)(q0 >> 16)))
+                                                 : 0u;
+                        const uint32_t h1 = real ? __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(
+                                                       (float)(int16_t)(q1 & 0xFFFF), (float)(int16_t)(q1 >> 16)))
+                                                 : 0u;
+                        // element 16t + 4u of the group: quarter 4t + u of
+                        // quantize_frag_kernel (slice 2 (t & 1) + u / 2, half t / 2)
+                        const int sl = 2 * (t & 1) + (u >> 1), hh = t >> 1;
+                        const size_t piece = (((size_t)mt * Kgo + go) * 4 + sl) * 64 + r + 32 * hh;
+                        *reinterpret_cast<uint2 *>(reinterpret_cast<char *>(a.hq) + piece * 16 + 8 * (u & 1)) =
+                            make_uint2(h0, h1);
+                    }
+                    if (u == 0) {
+                        const int ah = (r >> 2) & 1, e = 4 * (r >> 3) + (r & 3);
+                        a.hqs[(((size_t)mt * Kgo + go) * 2 + ah) * 16 + e] = real ? sc : 0.0f;
+                    }
+                }
+            }
+            return;
+        }
+    }
+
     // ---- store (an argmax caller that wants no logits passes C = null)
     if (!a.C) return;  // uniform
 #pragma unroll
@@ -586,7 +675,8 @@ __global__ __launch_bounds__(256, BPC) void gemm_mf_kernel(
     }
 }
 
-template <int TM, int TN, bool SWIGLU, int D, int BPC, int WM = 2, bool AL = true, int SG = kWsTile>
+template <int TM, int TN, bool SWIGLU, int D, int BPC, int WM = 2, bool AL = true, int SG = kWsTile,
+          bool HQ = false>
 static hipError_t launch_mf(const GemmMfArgs &a, hipStream_t st) {
     constexpr int BN = 32 * (4 / WM) * TN, MTB = WM * TM;
     const int ncols = SWIGLU ? BN / 2 : BN;
@@ -595,7 +685,7 @@ static hipError_t launch_mf(const GemmMfArgs &a, hipStream_t st) {
     const int tiles = ((a.N + ncols - 1) / ncols) * ((a.Mt + MTB - 1) / MTB);
     const int grid = 8 * ((tiles + 7) / 8);  // see the tile order in the kernel
     const size_t lds = 2 * (BN / 32) * 4 * 64 * 16 + (AL ? 2 * MTB * 4096 : 0) + 2 * 32 * MTB * 4 + 2 * SG * BN * 4;
-    gemm_mf_kernel<TM, TN, SWIGLU, D, BPC, WM, AL, SG><<<grid, 256, lds, st>>>(
+    gemm_mf_kernel<TM, TN, SWIGLU, D, BPC, WM, AL, SG, HQ><<<grid, 256, lds, st>>>(
         a.Af, a.asf, a.W0, a.S0, a.Mt, a.N, a.K, a.M, a.W1, a);
     return hipGetLastError();
 }
@@ -627,6 +717,12 @@ int gemm_mf_argmax_cols(int M) { return (M + 31) / 32 == 1 ? 128 : 64; }
 hipError_t launch_gemm_mf(const GemmMfArgs &a, bool swiglu, int cus, hipStream_t st) {
     if (a.K % (64 * kWsTile) != 0 || a.K <= 0 || a.M < 1 || a.N < 1) return hipErrorInvalidValue;
     if (swiglu && a.part_val) return hipErrorInvalidValue;
+    // h quantized in the epilogue: SwiGLU only, whole 64-column groups
+    if (a.hq && (!swiglu || !a.hqs || a.N % 64 != 0)) return hipErrorInvalidValue;
+    if (swiglu && a.hq) {
+        if (mf_blocks(a, 1, 64) <= 3L * cus) return launch_mf<1, 2, true, 2, 3, 2, false, 8, true>(a, st);
+        return launch_mf<2, 2, true, 2, 2, 2, true, 8, true>(a, st);
+    }
     if (swiglu) {
         if (mf_blocks(a, 1, 64) <= 3L * cus) return launch_mf<1, 2, true, 2, 3, 2, false, 8>(a, st);
         return launch_mf<2, 2, true, 2, 2, 2, true, 8>(a, st);

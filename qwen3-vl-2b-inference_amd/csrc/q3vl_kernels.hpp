@@ -135,6 +135,12 @@ struct GemmMfArgs {
     // launch_argmax_final
     float *part_val = nullptr;
     int32_t *part_idx = nullptr;
+    // optional (swiglu, N % 64 == 0): H is not stored; instead it is
+    // quantized as launch_quantize_frag would quantize it, into hq
+    // [Mt][N/64][4][64][8] and hqs [Mt][N/64][2][16] (the operand of a GEMM
+    // with K = N)
+    _Float16 *hq = nullptr;
+    float *hqs = nullptr;
 };
 // Columns per argmax partial of launch_gemm_mf for an M-row plain product.
 int gemm_mf_argmax_cols(int M);

@@ -50,6 +50,8 @@ def _declare(lib):
         "q3vl_linear_i8_groups": (i, [_vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _vp, _sz, _vp]),
         "q3vl_linear_i8_multi": (i, [_vp, _sz, _sz, _sz, i, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
         "q3vl_linear_i8_swiglu": (i, [_vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _vp, _sz, _vp]),
+        "q3vl_mlp_i8": (i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _vp, _sz, _vp]),
+        "q3vl_mlp_workspace_bytes": (_sz, [_sz, _sz, _sz, _sz]),
         "q3vl_lm_head_argmax": (i, [_vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _vp, _sz, _vp]),
         "q3vl_argmax_rows": (i, [_vp, _vp, _sz, _sz, _vp, _sz, _vp]),
         "q3vl_swiglu": (i, [_vp, _vp, _sz, _vp]),
@@ -212,6 +214,31 @@ def linear_i8_swiglu(A, Wg, Sg, Wu, Su, gs, out=None, workspace=None, stream=Non
     rc = lib().q3vl_linear_i8_swiglu(_ptr(A), _ptr(Wg), _ptr(Sg), _ptr(Wu), _ptr(Su), _ptr(out),
                                      M, N, K, gs, wp, wb, _stream(stream))
     _check(rc)
+    return out
+
+
+def mlp_workspace_bytes(M, H, I, gs) -> int:
+    return lib().q3vl_mlp_workspace_bytes(M, H, I, gs)
+
+
+def mlp_i8(A, Wg, Sg, Wu, Su, Wd, Sd, gs, out=None, workspace=None, stream=None):
+    """The MLP block: Y = (silu(A Wg^T) * (A Wu^T)) Wd^T, A [M,H], Wg/Wu [I,H],
+    Wd [H,I]."""
+    torch = _torch()
+    _need(A, torch.float32, "A", 2)
+    for t, n in ((Wg, "Wg"), (Wu, "Wu"), (Wd, "Wd")):
+        _need(t, torch.int8, n, 2)
+    for t, n in ((Sg, "Sg"), (Su, "Su"), (Sd, "Sd")):
+        _need(t, torch.float32, n)
+    M, H = A.shape
+    I = Wg.shape[0]
+    if Wg.shape != (I, H) or Wu.shape != (I, H) or Wd.shape != (H, I):
+        raise ValueError("shape mismatch between A, Wg, Wu and Wd")
+    out = torch.empty((M, H), dtype=torch.float32, device=A.device) if out is None else out
+    _need(out, torch.float32, "out")
+    wp, wb = _ws(workspace)
+    _check(lib().q3vl_mlp_i8(_ptr(A), _ptr(Wg), _ptr(Sg), _ptr(Wu), _ptr(Su), _ptr(Wd), _ptr(Sd),
+                             _ptr(out), M, H, I, gs, wp, wb, _stream(stream)))
     return out
 
 

@@ -260,6 +260,49 @@ def test_swiglu_fused_parity(orc, M, N, K):
     np.testing.assert_array_equal(H.view(np.uint32), H_ref.view(np.uint32))
 
 
+# The MLP block (q3vl_mlp_i8): fused where M > 8, group 64 and H, I are
+# multiples of 512 (the gate|up GEMM's epilogue quantizes h for the down
+# GEMM, in its 64-row and, at M = 600 x I = 6144, its 128-row tiles; M = 9
+# leaves a block's second m-tile past the product); the two calls through an
+# h buffer elsewhere (M <= 8, I = 1088, group 32).
+MLP = [(512, 2048, 6144, 64), (100, 1024, 2048, 64), (9, 512, 512, 64), (600, 512, 6144, 64),
+       (33, 1024, 1536, 64), (8, 1024, 2048, 64), (64, 1024, 1088, 64), (64, 1024, 1024, 32)]
+
+
+def mlp_ref(orc, A, Wg, Sg, Wu, Su, Wd, Sd, gs):
+    h = orc.swiglu(orc.linear(A, Wg, Sg, gs), orc.linear(A, Wu, Su, gs))
+    return orc.linear(h, Wd, Sd, gs)
+
+
+@pytest.mark.parametrize("M,H,I,gs", MLP, ids=[str(c) for c in MLP])
+def test_mlp_parity(orc, M, H, I, gs):
+    A, Wg, Sg = make_case(300 + M, M, I, H, gs)
+    _, Wu, Su = make_case(301 + M, M, I, H, gs)
+    _, Wd, Sd = make_case(302 + M, M, H, I, gs)
+    Y = host(q.mlp_i8(dev(A), dev(Wg), dev(Sg), dev(Wu), dev(Su), dev(Wd), dev(Sd), gs))
+    assert_bits_equal(Y, mlp_ref(orc, A, Wg, Sg, Wu, Su, Wd, Sd, gs), f"mlp {M}x{H}x{I} gs{gs}")
+
+
+def test_mlp_extreme_rows(orc):
+    """h groups at the quantizer's edges through the fused epilogue: huge
+    activations (an h of +-inf or NaN: the saturating branch), tiny ones (the
+    1e-6 floor of the scale), with a caller workspace of the advertised size."""
+    M, H, I = 40, 512, 512
+    A, Wg, Sg = make_case(310, M, I, H, 64)
+    _, Wu, Su = make_case(311, M, I, H, 64)
+    _, Wd, Sd = make_case(312, M, H, I, 64)
+    A[0] = 1.0e18
+    A[1] = 1.0e-30
+    A[2, :64] = 3.0e5
+    A[3, 7] = np.nan
+    ws = torch.zeros(q.mlp_workspace_bytes(M, H, I, 64), dtype=torch.uint8, device="cuda")
+    Y = host(q.mlp_i8(dev(A), dev(Wg), dev(Sg), dev(Wu), dev(Su), dev(Wd), dev(Sd), 64, workspace=ws))
+    Y_ref = mlp_ref(orc, A, Wg, Sg, Wu, Su, Wd, Sd, 64)
+    nan = np.isnan(Y_ref)
+    assert nan.any() and np.array_equal(np.isnan(Y), nan)
+    np.testing.assert_array_equal(Y[~nan].view(np.uint32), Y_ref[~nan].view(np.uint32))
+
+
 def test_swiglu_standalone(orc):
     from golden.make_golden import swiglu_inputs
     g, u = swiglu_inputs()
