@@ -10,6 +10,8 @@
 // bit-exact with the CPU oracle in its fp16-cache mode.
 #include <float.h>
 
+#include <type_traits>
+
 #include "q3vl_device.hpp"
 #include "q3vl_kernels.hpp"
 
@@ -59,30 +61,37 @@ __device__ __forceinline__ uint16_t f2h(float f) {
 // second; waiting for the first batch before issuing the second avoids that.
 __device__ __forceinline__ void lgkm_wait0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
 
-// Four chain steps acc = fma(p_c of lane k of this row of 16 lanes, v_c, acc),
-// c = 0..3: v_fmac_f32 with the DPP row_newbcast:k operand, one instruction
-// per step (the row broadcast replaces an LDS read of p per step). One asm
-// block holds the four steps, so no wait states are placed between them; the
+// Sixteen chain steps acc = fma(p_c of lane k of this row of 16 lanes,
+// v[k - k0].c, acc) for k = k0 .. k0+3 (k0 a multiple of 4), c = 0..3:
+// v_fmac_f32 with the DPP row_newbcast:k operand, one instruction per step
+// (the row broadcast replaces an LDS read of p per step). One asm block
+// holds the sixteen steps, so no wait states are placed between them; the
 // caller keeps 2 instructions between a VALU write of p and its first use.
-#define Q3VL_FMAC4_BC(K)                                                                        \
-    case K:                                                                                     \
-        asm volatile("v_fmac_f32_dpp %0, %1, %5 row_newbcast:" #K " row_mask:0xf bank_mask:0xf\n\t" \
-                     "v_fmac_f32_dpp %0, %2, %6 row_newbcast:" #K " row_mask:0xf bank_mask:0xf\n\t" \
-                     "v_fmac_f32_dpp %0, %3, %7 row_newbcast:" #K " row_mask:0xf bank_mask:0xf\n\t" \
-                     "v_fmac_f32_dpp %0, %4, %8 row_newbcast:" #K " row_mask:0xf bank_mask:0xf"     \
-                     : "+v"(acc)                                                                \
-                     : "v"(p0), "v"(p1), "v"(p2), "v"(p3), "v"(v.x), "v"(v.y), "v"(v.z), "v"(v.w)); \
+#define Q3VL_F4(K, V0, V1, V2, V3)                                  \
+    "v_fmac_f32_dpp %0, %1, " V0 " row_newbcast:" #K " row_mask:0xf bank_mask:0xf\n\t" \
+    "v_fmac_f32_dpp %0, %2, " V1 " row_newbcast:" #K " row_mask:0xf bank_mask:0xf\n\t" \
+    "v_fmac_f32_dpp %0, %3, " V2 " row_newbcast:" #K " row_mask:0xf bank_mask:0xf\n\t" \
+    "v_fmac_f32_dpp %0, %4, " V3 " row_newbcast:" #K " row_mask:0xf bank_mask:0xf\n\t"
+#define Q3VL_FMAC16_BC(K0, K1, K2, K3)                                                        \
+    case K0:                                                                                 \
+        asm volatile(Q3VL_F4(K0, "%5", "%6", "%7", "%8") Q3VL_F4(K1, "%9", "%10", "%11", "%12") \
+                         Q3VL_F4(K2, "%13", "%14", "%15", "%16")                              \
+                             Q3VL_F4(K3, "%17", "%18", "%19", "%20")                          \
+                     : "+v"(acc)                                                              \
+                     : "v"(p0), "v"(p1), "v"(p2), "v"(p3), "v"(v[0].x), "v"(v[0].y),         \
+                       "v"(v[0].z), "v"(v[0].w), "v"(v[1].x), "v"(v[1].y), "v"(v[1].z),       \
+                       "v"(v[1].w), "v"(v[2].x), "v"(v[2].y), "v"(v[2].z), "v"(v[2].w),       \
+                       "v"(v[3].x), "v"(v[3].y), "v"(v[3].z), "v"(v[3].w));                   \
         break;
-__device__ __forceinline__ void fmac4_row_bcast(float &acc, float p0, float p1, float p2, float p3,
-                                                const float4 &v, int k) {
+__device__ __forceinline__ void fmac16_row_bcast(float &acc, float p0, float p1, float p2, float p3,
+                                                 const float4 *v, int k) {
     switch (k) {
-        Q3VL_FMAC4_BC(0) Q3VL_FMAC4_BC(1) Q3VL_FMAC4_BC(2) Q3VL_FMAC4_BC(3)
-        Q3VL_FMAC4_BC(4) Q3VL_FMAC4_BC(5) Q3VL_FMAC4_BC(6) Q3VL_FMAC4_BC(7)
-        Q3VL_FMAC4_BC(8) Q3VL_FMAC4_BC(9) Q3VL_FMAC4_BC(10) Q3VL_FMAC4_BC(11)
-        Q3VL_FMAC4_BC(12) Q3VL_FMAC4_BC(13) Q3VL_FMAC4_BC(14) Q3VL_FMAC4_BC(15)
+        Q3VL_FMAC16_BC(0, 1, 2, 3) Q3VL_FMAC16_BC(4, 5, 6, 7)
+        Q3VL_FMAC16_BC(8, 9, 10, 11) Q3VL_FMAC16_BC(12, 13, 14, 15)
     }
 }
-#undef Q3VL_FMAC4_BC
+#undef Q3VL_FMAC16_BC
+#undef Q3VL_F4
 
 __device__ __forceinline__ float readlane_f(float v, int lane) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
@@ -590,24 +599,27 @@ __global__ __launch_bounds__(ATT_HD) void attn_combine_kernel(
 //   out[d] = fma chain over t = 0..pos of p_t * v_t[d].
 // The chain is inherently sequential (one dependent FMA per position), so
 // everything else is arranged around it. Loads are issued at entry (the
-// position first, then chunk maxima, scores and the first V chunk, in order
-// of use), so the softmax runs while V is still arriving. V is widened to
-// fp32 into LDS, transposed ([d][t]) with 16-byte row writes of 4 positions;
-// later chunks are loaded by waves 2 and 3 while the chain runs, so the
-// chain wave issues no loads. The chains read 64 positions ahead with the
-// reads spread between the FMAs. e also lives lane-major (row j holds e_j,
-// e_{j+8}, ...), which the denominator's segmented sums read.
+// position first, then chunk maxima, the scores of the kvm heads and, in
+// the staging waves, the first V chunk, in order of use), so the softmax runs
+// while V is still arriving. The block's 8 waves (two per SIMD) share the
+// e pass; waves 2, 3, 6 and 7 stage V: widened to fp32 into LDS, transposed
+// ([d][t]) with 16-byte row writes of 4 positions, chunk 0 while waves 0 ..
+// kvm-1 form the denominators, later chunks while the chain runs, so the
+// chain wave issues no global loads. The chains read 64
+// positions ahead with the reads spread between the FMAs. e also lives
+// lane-major (row j holds e_j, e_{j+8}, ...), which the denominator's
+// segmented sums read.
 constexpr int PV_D = 16;
 constexpr int PV_TC = 1024;
-constexpr int PV_THREADS = 256;
+constexpr int PV_THREADS = 512;  // 8 waves, two per SIMD
 constexpr int PV_RS = PV_TC + 4;                    // floats per LDS row of vt
-// chunk 0 is staged by all waves (PV_Q0 quads a thread), later chunks by
-// waves 2 and 3 (PV_QN quads a thread)
-constexpr int PV_Q0 = PV_TC * (PV_D / 8) / PV_THREADS / 4;
-constexpr int PV_QN = 2 * PV_Q0;
-static_assert(4 * (PV_THREADS / 2) * PV_Q0 == PV_TC && 4 * (PV_THREADS / 4) * PV_QN == PV_TC,
-              "the staging quads cover the chunk");
-constexpr int PV_SREG = 4;  // float4 score groups held in registers per head (4096 positions)
+// every chunk is staged by waves 2, 3, 6 and 7 (PV_QN quads a thread)
+constexpr int PV_NST = PV_THREADS / 2;  // staging threads
+constexpr int PV_QN = PV_TC * (PV_D / 8) / PV_NST / 4;
+static_assert(4 * (PV_NST / 2) * PV_QN == PV_TC, "the staging quads cover the chunk");
+// float4 score groups per head held in registers from entry (2048
+// positions; later ones are loaded when n is known)
+constexpr int PV_SREG = 2;
 
 // V staging: thread (vsg, vb) of a staging group holds the 8-dim half vsg
 // of the NQ quads of positions 4*(vb + QSTR*q) + i (item 4q + i) of a
@@ -664,6 +676,7 @@ __host__ __device__ __forceinline__ int pv_et_stride(int max_seq) {
     return (max_seq / 8 + 31) / 32 * 32 + 4;
 }
 
+template <int KVM>
 __global__ __launch_bounds__(PV_THREADS) void attn_softmax_pv_kernel(
     const int32_t *pos_p, const float *scores_p, const float *cmax_p, const uint16_t *v_cache_p,
     int layer_p, int heads_p, int kv_heads_p, int max_seq_p, int max_chunks_p, AttnArgs args) {
@@ -678,7 +691,7 @@ __global__ __launch_bounds__(PV_THREADS) void attn_softmax_pv_kernel(
     a.max_seq = max_seq_p;
     a.max_chunks = max_chunks_p;
     extern __shared__ __align__(16) float smem[];
-    const int kvm = a.heads / a.kv_heads;
+    constexpr int kvm = KVM;  // query heads per kv head (a.heads / a.kv_heads)
     const int S = a.max_seq, ets = pv_et_stride(S);
     // e and et first: the chains' p reads then use small constant offsets
     float *e = smem;                        // [kvm][S]: e_t, then p_t
@@ -692,10 +705,9 @@ __global__ __launch_bounds__(PV_THREADS) void attn_softmax_pv_kernel(
     // ---- entry loads. The position's scalar load goes first (the vector
     // loads below can wait at issue for queue room, and it must not wait
     // behind them); the others follow in order of use, all issued before
-    // `pos` is known (their latency overlaps its own). Every load is
-    // unconditional, with indices clamped into the buffers, so no wait
-    // depends on which were issued; values past the context are masked once
-    // pos is known.
+    // `pos` is known (their latency overlaps its own). Indices are clamped
+    // into the buffers; values past the context are masked once pos is
+    // known.
     const int pos = *a.pos;
     __builtin_amdgcn_sched_barrier(0);
     // chunk maxima: wave hh < kvm, lane c (one pass covers 4096 positions)
@@ -706,90 +718,113 @@ __global__ __launch_bounds__(PV_THREADS) void attn_softmax_pv_kernel(
     // so the float4s past a multiple of PV_THREADS fall to wave 0 on one
     // head and to the last wave on the next, and no wave computes every
     // head's tail
-    float4 sreg[3][PV_SREG];
+    float4 sreg[kvm][PV_SREG];
 #pragma unroll
-    for (int hh = 0; hh < 3; ++hh) {
-        const float4 *sc = reinterpret_cast<const float4 *>(a.scores + (size_t)(kvh * kvm + min(hh, kvm - 1)) * S);
+    for (int hh = 0; hh < kvm; ++hh) {
+        const float4 *sc = reinterpret_cast<const float4 *>(a.scores + (size_t)(kvh * kvm + hh) * S);
         const int ti = (hh & 1) ? PV_THREADS - 1 - tid : tid;
 #pragma unroll
         for (int k = 0; k < PV_SREG; ++k) sreg[hh][k] = sc[min(ti + PV_THREADS * k, S / 4 - 1)];
     }
-    // V chunk 0: every thread loads its share at entry (thread tid: vsg =
-    // tid & 1, vb = tid >> 1, quads vb and vb + 128) and widens it into LDS
-    // after its softmax work. Later chunks: waves 2 and 3 (staging thread
-    // tid & 127: vb = (tid & 127) >> 1, quads vb + 64q) load them while the
-    // chain runs on the previous one, so the chain wave issues no loads.
-    u32x4 vr0[4 * PV_Q0], vrn[4 * PV_QN];
-    const int vsg = tid & 1;
+    // V: waves 2, 3, 6 and 7 stage every chunk (staging thread s = 64
+    // (wid & 1 | wid / 4 * 2) + lane: vsg = s & 1, vb = s >> 1, quads vb +
+    // PV_NST/2 q), chunk 0 loaded here and widened into LDS while waves 0 ..
+    // kvm-1 form the denominators, each later chunk loaded while the chain
+    // runs on the one before, so the chain wave issues no global loads. The
+    // other waves load no V. (Waves go to the CU's four SIMDs in turn, wave w
+    // to SIMD w % 4: the stagers then share SIMDs 2 and 3, and the sums and
+    // the chain, on SIMDs 0 and 1, share theirs with waves 4 and 5, idle by
+    // then.)
+    u32x4 vrn[4 * PV_QN];
     const int wu = __builtin_amdgcn_readfirstlane(wid);  // wave-uniform
-    const bool stager = wu >= 2;
-    __builtin_amdgcn_sched_barrier(0);
-    pv_load<PV_Q0, PV_THREADS / 2>(vr0, vc, 0, S, vsg, tid >> 1);
-    __builtin_amdgcn_sched_barrier(0);
-
-    if (pos < 0 || pos >= S) {  // no cache row for it: NaN outputs
-        if (wid == 0 && (lane >> 4) < kvm)
-            a.out[(kvh * kvm + (lane >> 4)) * ATT_HD + db * PV_D + (lane & 15)] = __builtin_nanf("");
-        return;
-    }
+    const bool stager = (wu & 2) != 0;
+    const int vsg = tid & 1, vb = ((((wu & 1) | (wu >> 2) << 1)) * 64 + lane) >> 1;
     const int n = pos + 1;
     const int nb = n & ~7;
     const int nch = (n + ATT_CH - 1) / ATT_CH;
     auto chunk_lim = [&](int t0) { return (min(PV_TC, n - t0) + 63) & ~63; };
 
-    // ---- M per head from the chunk maxima (beyond one pass: loop)
-    if (wid < kvm) {
-        const float *cmh = a.cmax + (kvh * kvm + wid) * a.max_chunks;
-        float m = lane < nch ? cm : -INFINITY;  // loaded for head wh == wid
-        for (int c = lane + 64; c < nch; c += 64) m = fmaxf(m, cmh[c]);
-        m = wave_max(m);  // (any order: DPP moves, no LDS round trips)
-        if (lane == 0) hmax[wid] = m;
+    // The position check, M and the e pass, written out once for the
+    // stagers (with their V loads) and once for the other waves: the
+    // compiler's wait counts at a join cover the loads of either path, so
+    // one copy after a conditional V load would make the stagers' first
+    // score use wait for the V transfer too. The stagers issue V after the
+    // barrier that follows M, when every wave's entry loads have gone out:
+    // issued at entry, V's many cache lines held the later waves' chunk
+    // maxima and scores back in the CU's memory pipeline, and the barrier
+    // with them. Returns false when pos has no cache row.
+    float Mw = 0.0f;  // M of head wid, in waves wid < kvm
+    auto front = [&](auto stg) -> bool {
+        if (pos < 0 || pos >= S) {  // no cache row for it: NaN outputs
+            if (wid == 0 && (lane >> 4) < kvm)
+                a.out[(kvh * kvm + (lane >> 4)) * ATT_HD + db * PV_D + (lane & 15)] = __builtin_nanf("");
+            return false;
+        }
+        // ---- M per head from the chunk maxima (beyond one pass: loop)
+        if (wid < kvm) {
+            const float *cmh = a.cmax + (kvh * kvm + wid) * a.max_chunks;
+            float m = lane < nch ? cm : -INFINITY;  // loaded for head wh == wid
+            for (int c = lane + 64; c < nch; c += 64) m = fmaxf(m, cmh[c]);
+            m = wave_max(m);  // (any order: DPP moves, no LDS round trips)
+            if (lane == 0) hmax[wid] = m;
+            Mw = m;
+        }
+        lds_barrier();
+        if constexpr (decltype(stg)::value) {
+            __builtin_amdgcn_sched_barrier(0);
+            pv_load<PV_QN, PV_NST / 2>(vrn, vc, 0, S, vsg, vb);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        // ---- e_t (text_layer.cpp:486-493, 501-509), stored both ways,
+        // computed and selected without per-position branches
+#pragma unroll
+        for (int hh = 0; hh < kvm; ++hh) {
+            const float M = hmax[hh];
+            const bool fin = __builtin_isfinite(M);
+            float *eh = e + hh * S, *eth = et + hh * 8 * ets;
+            auto ev_of = [&](float v) {
+                const float x = exp256(v - M);
+                return (fin && v > -INFINITY) ? x : 0.0f;
+            };
+            auto put4 = [&](int t, float4 v) {  // positions t..t+3, t % 4 == 0
+                float4 ev;
+                ev.x = ev_of(v.x);
+                ev.y = ev_of(v.y);
+                ev.z = ev_of(v.z);
+                ev.w = ev_of(v.w);
+                if (t < n) *reinterpret_cast<float4 *>(eh + t) = ev;  // t + 3 < S
+                if (t < nb) {  // nb % 8 == 0: all four below nb
+                    const int c = t >> 3, j = t & 7;
+                    eth[(j + 0) * ets + c] = ev.x;
+                    eth[(j + 1) * ets + c] = ev.y;
+                    eth[(j + 2) * ets + c] = ev.z;
+                    eth[(j + 3) * ets + c] = ev.w;
+                }
+            };
+            // zeros after the lane sums' last term, up to a whole batch of
+            // 32 per lane: adding +0 to a sum of non-negative terms is exact
+            const int zend = (nb + 255) & ~255;
+            for (int t = nb + tid; t < zend; t += PV_THREADS) eth[(t & 7) * ets + (t >> 3)] = 0.0f;
+            // a wave skips a k with no position below n (uniform: its lowest
+            // float4 index is 64*wid + PV_THREADS*k, mirrored on odd heads)
+            const int ti = (hh & 1) ? PV_THREADS - 1 - tid : tid;
+            const int wlo = (hh & 1) ? PV_THREADS - 64 * (wu + 1) : 64 * wu;
+#pragma unroll
+            for (int k = 0; k < PV_SREG; ++k)
+                if (4 * (wlo + PV_THREADS * k) < n) put4(4 * (ti + PV_THREADS * k), sreg[hh][k]);
+            const float4 *sc = reinterpret_cast<const float4 *>(a.scores + (size_t)(kvh * kvm + hh) * S);
+            for (int i = tid + PV_THREADS * PV_SREG; 4 * i < n; i += PV_THREADS) put4(4 * i, sc[i]);
+        }
+        return true;
+    };
+    if (stager) {
+        if (!front(std::true_type{})) return;
+    } else {
+        if (!front(std::false_type{})) return;
     }
     lds_barrier();
-    // ---- e_t (text_layer.cpp:486-493, 501-509), stored both ways, computed
-    // and selected without per-position branches
-#pragma unroll
-    for (int hh = 0; hh < 3; ++hh) {
-        if (hh >= kvm) break;  // uniform
-        const float M = hmax[hh];
-        const bool fin = __builtin_isfinite(M);
-        float *eh = e + hh * S, *eth = et + hh * 8 * ets;
-        auto ev_of = [&](float v) {
-            const float x = exp256(v - M);
-            return (fin && v > -INFINITY) ? x : 0.0f;
-        };
-        auto put4 = [&](int t, float4 v) {  // positions t..t+3, t % 4 == 0
-            float4 ev;
-            ev.x = ev_of(v.x);
-            ev.y = ev_of(v.y);
-            ev.z = ev_of(v.z);
-            ev.w = ev_of(v.w);
-            if (t < n) *reinterpret_cast<float4 *>(eh + t) = ev;  // t + 3 < S
-            if (t < nb) {  // nb % 8 == 0: all four below nb
-                const int c = t >> 3, j = t & 7;
-                eth[(j + 0) * ets + c] = ev.x;
-                eth[(j + 1) * ets + c] = ev.y;
-                eth[(j + 2) * ets + c] = ev.z;
-                eth[(j + 3) * ets + c] = ev.w;
-            }
-        };
-        // zeros after the lane sums' last term, up to a whole batch of 32
-        // per lane: adding +0 to a sum of non-negative terms is exact
-        const int zend = (nb + 255) & ~255;
-        for (int t = nb + tid; t < zend; t += PV_THREADS) eth[(t & 7) * ets + (t >> 3)] = 0.0f;
-        // a wave skips a k with no position below n (uniform: its lowest
-        // float4 index is 64*wid + PV_THREADS*k, mirrored on odd heads)
-        const int ti = (hh & 1) ? PV_THREADS - 1 - tid : tid;
-        const int wlo = (hh & 1) ? PV_THREADS - 64 * (wu + 1) : 64 * wu;
-#pragma unroll
-        for (int k = 0; k < PV_SREG; ++k)
-            if (4 * (wlo + PV_THREADS * k) < n) put4(4 * (ti + PV_THREADS * k), sreg[hh][k]);
-        const float4 *sc = reinterpret_cast<const float4 *>(a.scores + (size_t)(kvh * kvm + hh) * S);
-        for (int i = tid + PV_THREADS * PV_SREG; 4 * i < n; i += PV_THREADS) put4(4 * i, sc[i]);
-    }
-    lds_barrier();
-    // ---- sums and the fp32 inverse, one wave per head; waves 2 and 3 widen
-    // V chunk 0 into LDS meanwhile. Lane sum l (the sequential fp32 sum over
+    // ---- sums and the fp32 inverse, one wave per head; the staging waves
+    // widen V chunk 0 into LDS meanwhile. Lane sum l (the sequential fp32 sum over
     // t = l mod 8) is cut into segments of 32 terms; in a pass over 256 terms
     // lane 8l+s holds segment s of sum l in registers. Every lane adds its
     // segment's terms in each round, and a DPP row shift hands each lane's
@@ -828,34 +863,42 @@ __global__ __launch_bounds__(PV_THREADS) void attn_softmax_pv_kernel(
             }
             last = nr - 1;
         }
+        // the 8 lane sums, then the tail terms, in double and in order; the
+        // terms are gathered first so that only the adds form the chain, and
+        // all 7 tail lanes are added (0 past pos: adding +0 to the sum, never
+        // -0, leaves it unchanged)
+        float part[15];
+#pragma unroll
+        for (int l = 0; l < 8; ++l) part[l] = readlane_f(acc, 8 * l + last);  // lane sum l
+#pragma unroll
+        for (int l = 0; l < 7; ++l) part[8 + l] = readlane_f(tl, l);
         double sum = 0.0;
 #pragma unroll
-        for (int l = 0; l < 8; ++l) sum += (double)readlane_f(acc, 8 * l + last);  // lane sum l
-#pragma unroll
-        for (int l = 0; l < 7; ++l)
-            if (l < n - nb) sum += (double)readlane_f(tl, l);
-        const bool ok = __builtin_isfinite(hmax[wid]) && sum > 0.0 && __builtin_isfinite(sum);
+        for (int i = 0; i < 15; ++i) sum += (double)part[i];
+        const bool ok = __builtin_isfinite(Mw) && sum > 0.0 && __builtin_isfinite(sum);
         const float inv = ok ? (float)(1.0 / sum) : 0.0f;
         if (lane == 0) hinv[wid] = inv;
     }
-    pv_store<PV_Q0, PV_THREADS / 2>(vt, vr0, vsg, tid >> 1, 0, chunk_lim(0), pos);  // V chunk 0
+    if (stager) pv_store<PV_QN, PV_NST / 2>(vt, vrn, vsg, vb, 0, chunk_lim(0), pos);  // V chunk 0
 
     // ---- value-weighted sums. Wave 0 runs the chains: row r of 16 lanes is
     // query head r, lane d of the row output dim db*PV_D + d. Per batch of 64
     // positions tb..tb+63, lane k of a row holds p_{tb+4k+c} = e * inv
     // (c < 4, formed in registers; 0 past the context, which leaves the
     // chain unchanged: acc is never -0, and fma(0, v, acc) = acc for finite
-    // v) and every step broadcasts one of them across the row.
+    // v) and every step broadcasts one of them across the row. Only the
+    // chunk's last batch can reach past the context, so only it masks p by
+    // position.
     const int rl = lane & 15, hrow = min(lane >> 4, kvm - 1);
     const bool chain = wid == 0 && (lane >> 4) < kvm;
     float acc = 0.0f;
     for (int t0 = 0; t0 < n; t0 += PV_TC) {
         if (t0 > 0) {
             lds_barrier();  // previous chains done with vt
-            if (stager) pv_store<PV_QN, PV_THREADS / 4>(vt, vrn, vsg, (tid & 127) >> 1, t0, chunk_lim(t0), pos);
+            if (stager) pv_store<PV_QN, PV_NST / 2>(vt, vrn, vsg, vb, t0, chunk_lim(t0), pos);
         }
         lds_barrier();      // vt (and inv) ready
-        if (stager && t0 + PV_TC < n) pv_load<PV_QN, PV_THREADS / 4>(vrn, vc, t0 + PV_TC, S, vsg, (tid & 127) >> 1);
+        if (stager && t0 + PV_TC < n) pv_load<PV_QN, PV_NST / 2>(vrn, vc, t0 + PV_TC, S, vsg, vb);
         if (chain) {
             const float invh = hinv[hrow];
             const float *eph = e + hrow * S + t0;
@@ -872,36 +915,55 @@ __global__ __launch_bounds__(PV_THREADS) void attn_softmax_pv_kernel(
             // the reference zeroes its p (text_layer.cpp:512-515), and e * 0
             // would be NaN for an e of -inf
             const bool live = invh > 0.0f;
-            auto run64 = [&](const float4 &E, const float4 *V, int tb) {
-                const int t = tb + 4 * rl;
-                const float p0 = live && t + 0 < len ? E.x * invh : 0.0f;
-                const float p1 = live && t + 1 < len ? E.y * invh : 0.0f;
-                const float p2 = live && t + 2 < len ? E.z * invh : 0.0f;
-                const float p3 = live && t + 3 < len ? E.w * invh : 0.0f;
+            auto run64 = [&](const float4 &E, const float4 *V, int tb, auto last_c) {
+                float p0, p1, p2, p3;
+                if constexpr (decltype(last_c)::value) {
+                    const int t = tb + 4 * rl;
+                    p0 = live && t + 0 < len ? E.x * invh : 0.0f;
+                    p1 = live && t + 1 < len ? E.y * invh : 0.0f;
+                    p2 = live && t + 2 < len ? E.z * invh : 0.0f;
+                    p3 = live && t + 3 < len ? E.w * invh : 0.0f;
+                } else {  // every position of the batch is below len
+                    p0 = live ? E.x * invh : 0.0f;
+                    p1 = live ? E.y * invh : 0.0f;
+                    p2 = live ? E.z * invh : 0.0f;
+                    p3 = live ? E.w * invh : 0.0f;
+                }
                 asm volatile("s_nop 1" ::"v"(p0), "v"(p1), "v"(p2), "v"(p3));  // DPP read-after-write
 #pragma unroll
-                for (int k = 0; k < 16; ++k) fmac4_row_bcast(acc, p0, p1, p2, p3, V[k], k);
+                for (int k = 0; k < 16; k += 4) fmac16_row_bcast(acc, p0, p1, p2, p3, V + k, k);
             };
+            const std::integral_constant<bool, false> full{};
+            const std::integral_constant<bool, true> last{};
             // batches of 64 in two register sets used in turn: the next
-            // batch's LDS reads are issued before the current batch's steps
-            const int nbat = (len + 63) >> 6;
+            // batch's LDS reads are issued before the current batch's
+            // steps; batches 0 .. nbat-2 are whole, nbat-1 the last
+            const int nbat = (len + 63) >> 6, nfull = nbat - 1;
             ld(Ae, Av, 0);
             int bi = 0;
-            for (; bi + 2 <= nbat; bi += 2) {
+            for (; bi + 2 <= nfull; bi += 2) {
                 lgkm_wait0();
                 __builtin_amdgcn_sched_barrier(0);
                 ld(Be, Bv, 64 * (bi + 1));
-                run64(Ae, Av, 64 * bi);
+                run64(Ae, Av, 64 * bi, full);
                 __builtin_amdgcn_sched_barrier(0);
                 lgkm_wait0();
                 __builtin_amdgcn_sched_barrier(0);
-                ld(Ae, Av, 64 * min(bi + 2, nbat - 1));
-                run64(Be, Bv, 64 * (bi + 1));
+                ld(Ae, Av, 64 * (bi + 2));  // bi + 2 <= nfull < nbat
+                run64(Be, Bv, 64 * (bi + 1), full);
                 __builtin_amdgcn_sched_barrier(0);
             }
-            if (bi < nbat) {  // A holds the last batch
+            if (bi < nfull) {  // A holds whole batch bi, the last is bi + 1
                 lgkm_wait0();
-                run64(Ae, Av, 64 * bi);
+                __builtin_amdgcn_sched_barrier(0);
+                ld(Be, Bv, 64 * (bi + 1));
+                run64(Ae, Av, 64 * bi, full);
+                __builtin_amdgcn_sched_barrier(0);
+                lgkm_wait0();
+                run64(Be, Bv, 64 * (bi + 1), last);
+            } else {  // A holds the last batch
+                lgkm_wait0();
+                run64(Ae, Av, 64 * bi, last);
             }
         }
     }
@@ -918,6 +980,18 @@ hipError_t launch_embed(const int8_t *w, const float *s, const int32_t *token, f
 size_t attention_lds_bytes(int heads, int kv_heads, int max_seq) {
     const size_t kvm = (size_t)(heads / kv_heads);
     return (size_t)PV_D * PV_RS * 4 + kvm * max_seq * 4 + kvm * 8 * (size_t)pv_et_stride(max_seq) * 4;
+}
+
+template <int KVM>
+static hipError_t launch_softmax_pv(const AttnArgs &a, size_t lds, hipStream_t st) {
+    // raise the dynamic LDS limit once per process and instantiation
+    static const hipError_t attr = hipFuncSetAttribute(
+        reinterpret_cast<const void *>(&attn_softmax_pv_kernel<KVM>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, (int)kAttnMaxLds);
+    if (attr != hipSuccess) return attr;
+    attn_softmax_pv_kernel<KVM><<<dim3(a.kv_heads, ATT_HD / PV_D), PV_THREADS, lds, st>>>(
+        a.pos, a.scores, a.cmax, a.v_cache, a.layer, a.heads, a.kv_heads, a.max_seq, a.max_chunks, a);
+    return hipGetLastError();
 }
 
 hipError_t launch_attention(const AttnArgs &a, hipStream_t st) {
@@ -941,16 +1015,11 @@ hipError_t launch_attention(const AttnArgs &a, hipStream_t st) {
         a.pos, a.k_cache, a.q, a.k, a.qnorm_w, a.layer, a.heads, a.kv_heads, a.max_seq, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    static int lds_set = 0;  // raise the dynamic LDS limit once per process
-    if (!lds_set) {
-        e = hipFuncSetAttribute(reinterpret_cast<const void *>(&attn_softmax_pv_kernel),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)kAttnMaxLds);
-        if (e != hipSuccess) return e;
-        lds_set = 1;
+    switch (kvm) {
+    case 1: return launch_softmax_pv<1>(a, lds, st);
+    case 2: return launch_softmax_pv<2>(a, lds, st);
+    default: return launch_softmax_pv<3>(a, lds, st);
     }
-    attn_softmax_pv_kernel<<<dim3(a.kv_heads, ATT_HD / PV_D), PV_THREADS, lds, st>>>(
-        a.pos, a.scores, a.cmax, a.v_cache, a.layer, a.heads, a.kv_heads, a.max_seq, a.max_chunks, a);
-    return hipGetLastError();
 }
 
 }  // namespace q3vl
