@@ -931,7 +931,12 @@ __global__ __launch_bounds__(PV_THREADS) void attn_softmax_pv_kernel(
                 }
                 asm volatile("s_nop 1" ::"v"(p0), "v"(p1), "v"(p2), "v"(p3));  // DPP read-after-write
 #pragma unroll
-                for (int k = 0; k < 16; k += 4) fmac16_row_bcast(acc, p0, p1, p2, p3, V + k, k);
+                for (int k = 0; k < 16; k += 4) {
+                    // the last batch stops at the first block of 16 steps
+                    // wholly past the context (their p are 0: no change)
+                    if (decltype(last_c)::value && tb + 4 * k >= len) break;  // uniform
+                    fmac16_row_bcast(acc, p0, p1, p2, p3, V + k, k);
+                }
             };
             const std::integral_constant<bool, false> full{};
             const std::integral_constant<bool, true> last{};

@@ -1216,41 +1216,71 @@ __device__ void am_block_reduce(float &bv, int32_t &bi) {
 
 // Reduces block partials [nparts, M] to ids[m] (empty partials have idx < 0;
 // none at all -> 0, as greedy_decode returns 0 when nothing beats -FLT_MAX).
-// One 1024-thread block per row m, each thread issuing all of its (<= 8)
-// loads before combining.
-__global__ __launch_bounds__(1024) void argmax_final_kernel(const float *pv, const int32_t *pi,
-                                                            int nparts, int M, int32_t *ids,
-                                                            int32_t *pos_inc) {
-    __shared__ float wv[16];
-    __shared__ int32_t wi[16];
-    const int tid = threadIdx.x;
+// One 256-thread block per row m: each thread issues all of its loads of a
+// pass (8 partials, indices clamped into the buffer, so every load is
+// unconditional) before combining them, then each wave reduces by DPP moves
+// (quad swaps and row mirrors, then the four rows' lane 0) and lane 0 of
+// wave 0 combines the four waves. The combine (larger value, then lower
+// index, empties ignored) selects one element of a total order, so any
+// reduction order gives the same (value, index).
+__global__ __launch_bounds__(256) void argmax_final_kernel(const float *pv, const int32_t *pi,
+                                                           int nparts, int M, int32_t *ids,
+                                                           int32_t *pos_inc) {
+    __shared__ float wv[4];
+    __shared__ int32_t wi[4];
+    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
     const int m = blockIdx.x;
-    float v[8];
-    int32_t ix[8];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-        const int p = tid + u * 1024;
-        v[u] = p < nparts ? pv[(size_t)p * M + m] : -FLT_MAX;
-        ix[u] = p < nparts ? pi[(size_t)p * M + m] : -1;
-    }
     float bv = -FLT_MAX;
     int32_t bi = -1;
+    for (int p0 = 0; p0 < nparts; p0 += 8 * 256) {
+        float v[8];
+        int32_t ix[8];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) am_combine(bv, bi, v[u], ix[u]);
+        for (int u = 0; u < 8; ++u) {
+            const int p = p0 + tid + u * 256;
+            const size_t at = (size_t)min(p, nparts - 1) * M + m;
+            v[u] = pv[at];
+            ix[u] = pi[at];
+        }
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        const float ov = __shfl_xor(bv, off);
-        const int32_t oi = __shfl_xor(bi, off);
+        for (int u = 0; u < 8; ++u) am_combine(bv, bi, v[u], p0 + tid + u * 256 < nparts ? ix[u] : -1);
+    }
+#define Q3VL_DPPV(x, ctrl) \
+    __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), ctrl, 0xF, 0xF, false))
+#define Q3VL_DPPI(x, ctrl) __builtin_amdgcn_mov_dpp(x, ctrl, 0xF, 0xF, false)
+    // quad_perm [1,0,3,2], [2,3,0,1], row_half_mirror, row_mirror: every lane
+    // of a row of 16 ends with the row's combine
+    {
+        float ov = Q3VL_DPPV(bv, 0xB1);
+        int32_t oi = Q3VL_DPPI(bi, 0xB1);
+        am_combine(bv, bi, ov, oi);
+        ov = Q3VL_DPPV(bv, 0x4E);
+        oi = Q3VL_DPPI(bi, 0x4E);
+        am_combine(bv, bi, ov, oi);
+        ov = Q3VL_DPPV(bv, 0x141);
+        oi = Q3VL_DPPI(bi, 0x141);
+        am_combine(bv, bi, ov, oi);
+        ov = Q3VL_DPPV(bv, 0x140);
+        oi = Q3VL_DPPI(bi, 0x140);
         am_combine(bv, bi, ov, oi);
     }
-    if ((tid & 63) == 0) {
-        wv[tid >> 6] = bv;
-        wi[tid >> 6] = bi;
+#undef Q3VL_DPPV
+#undef Q3VL_DPPI
+    auto rdv = [&](int l) {
+        return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, bv), l));
+    };
+    float rv = rdv(0);
+    int32_t ri = __builtin_amdgcn_readlane(bi, 0);
+#pragma unroll
+    for (int r = 1; r < 4; ++r) am_combine(rv, ri, rdv(16 * r), __builtin_amdgcn_readlane(bi, 16 * r));
+    if (lane == 0) {
+        wv[wid] = rv;
+        wi[wid] = ri;
     }
     __syncthreads();
     if (tid == 0) {
-        for (int w = 1; w < 16; ++w) am_combine(bv, bi, wv[w], wi[w]);
-        ids[m] = bi < 0 ? 0 : bi;
+        for (int w = 1; w < 4; ++w) am_combine(rv, ri, wv[w], wi[w]);
+        ids[m] = ri < 0 ? 0 : ri;
         if (pos_inc && m == 0) *pos_inc += 1;
     }
 }
@@ -1591,7 +1621,7 @@ hipError_t launch_argmax_final(const float *pv, const int32_t *pi, int nparts, i
                                int32_t *ids, hipStream_t st, int32_t *pos_inc) {
     if (nparts > 8192) return hipErrorInvalidValue;
     if (M < 1) return hipErrorInvalidValue;
-    argmax_final_kernel<<<M, 1024, 0, st>>>(pv, pi, nparts, M, ids, pos_inc);
+    argmax_final_kernel<<<M, 256, 0, st>>>(pv, pi, nparts, M, ids, pos_inc);
     return hipGetLastError();
 }
 
