@@ -395,6 +395,26 @@ def test_lm_head_argmax_gemm_path(orc, M, V, K):
     np.testing.assert_array_equal(ids, ids_ref)
 
 
+def test_lm_head_argmax_partials_over_passes(orc):
+    """M = 40 on the GEMM path leaves one argmax partial per 64 columns: at
+    V = 140000 that is 2188 partials, more than the final reduction's first
+    pass of 2048. Row 0's winner copied into a column of the second pass
+    (>= 131072) and to a lower column of the first: the lower one must win
+    across the passes; every row's id equals the oracle's scan."""
+    M, V, K, gs = 40, 140000, 1024, 64
+    A, W, S = make_case(4343, M, V, K, gs)
+    top = int(orc.argmax_rows(orc.linear(A[:1], W, S, gs))[0])
+    hi, lo = 139000, 5000
+    for r in (hi, lo):
+        W[r] = W[top]
+        S[r] = S[top]
+    logits_ref = orc.linear(A, W, S, gs)
+    ids_ref = orc.argmax_rows(logits_ref)
+    assert ids_ref[0] == min(lo, top) and logits_ref[0, hi] == logits_ref[0, lo]
+    ids = host(q.lm_head_argmax(dev(A), dev(W), dev(S), gs))
+    np.testing.assert_array_equal(ids, ids_ref)
+
+
 def test_lm_head_argmax_gemm_special_values(orc):
     """Argmax partials fused into the GEMM: a row of NaN logits (id 0), a
     column made +-inf/NaN by an infinite weight scale, a column whose logits
