@@ -1044,6 +1044,10 @@ def trace_summary(path):
     for tag, rs in regions.items():
         out[f"region {tag}"] = agg(rs)
         out[f"region {tag} total_us"] = round(sum((t1 - t0) / 1000.0 for t0, t1, _, _ in rs), 1)
+        # wall time from the region's first dispatch to its last one's end:
+        # the timed replays including their launch gaps
+        if rs:
+            out[f"region {tag} wall_us"] = round((max(t1 for _, t1, _, _ in rs) - rs[0][0]) / 1000.0, 1)
     out["whole_run"] = agg(rows)
     return out
 
