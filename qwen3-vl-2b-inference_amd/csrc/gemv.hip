@@ -1619,7 +1619,8 @@ hipError_t launch_gemv(const GemvArgs &a, bool lanes, int *grid_out, hipStream_t
 
 hipError_t launch_argmax_final(const float *pv, const int32_t *pi, int nparts, int M,
                                int32_t *ids, hipStream_t st, int32_t *pos_inc) {
-    if (nparts > 8192) return hipErrorInvalidValue;
+    // (the kernel clamps its loads to partial nparts - 1: at least one)
+    if (nparts < 1 || nparts > 8192) return hipErrorInvalidValue;
     if (M < 1) return hipErrorInvalidValue;
     argmax_final_kernel<<<M, 256, 0, st>>>(pv, pi, nparts, M, ids, pos_inc);
     return hipGetLastError();
