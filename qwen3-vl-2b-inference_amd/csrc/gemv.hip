@@ -1490,7 +1490,15 @@ static StreamCfg stream_cfg(const GemvArgs &a) {
     if (a.K == 6144) return {8, 1, 0};
     int rows = 0;
     for (int s = 0; s < a.nseg; ++s) rows += a.seg[s].N;
-    return rows > 2048 ? StreamCfg{8, 2, 0} : StreamCfg{8, 1, 0};
+    if (rows <= 2048) return {8, 1, 0};
+    // 3-row tiles where 2-row tiles would need more than one 8-wave block
+    // per CU and 3-row tiles need at most one (6144 rows: 256 blocks instead
+    // of 384, half the CUs holding two; graph replay from HBM 5.2 -> 4.9 us)
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) == hipSuccess && device_cus(dev, &cus) == hipSuccess && a.nseg == 1 &&
+        (rows + 15) / 16 > cus && (rows + 23) / 24 <= cus)
+        return {8, 3, 0};
+    return {8, 2, 0};
 }
 
 static size_t stream_lds(int KC, int R, int NW) {
@@ -1533,6 +1541,7 @@ static hipError_t launch_stream_md(const GemvArgs &a, const StreamCfg &c, int *g
     if constexpr (MD != MD_SWIGLU) {
         Q3VL_STREAM(1, 4)
         Q3VL_STREAM(1, 8)
+        if constexpr (KC == 2048) Q3VL_STREAM(3, 8)
     }
     Q3VL_STREAM(2, 4)
     Q3VL_STREAM(2, 8)

@@ -115,7 +115,10 @@ def test_lane_gemv_parity(orc, M, N, K, gs):
 # The decode step's row lengths at group 64 without group-sum output: the
 # streaming kernel (one wave per row tile, tiles looped per wave), with ragged
 # last tiles and more tiles than waves.
+# (4100, 5000 and 6144 rows at K = 2048 run 3-row tiles on a 256-CU device,
+# the first two with a partial last tile)
 STREAM = [(1, 1024, 2048), (1, 1029, 2048), (1, 2050, 2048), (1, 4096, 2048), (1, 9001, 2048),
+          (1, 4100, 2048), (1, 5000, 2048), (1, 6144, 2048),
           (1, 1024, 6144), (1, 1031, 6144), (1, 2048, 6144), (1, 6145, 6144)]
 
 
