@@ -274,8 +274,33 @@ int run_linear(const float *A, int nseg, const int8_t *const *W, const float *co
         use_mf = !(G && G[i]) && (size_t)Ns[i] * K <= 0x7fffffffULL &&
                  gemm_mf_serves((int)M, (int)Ns[i], (int)K, mode == GEMV_SWIGLU, cus);
     if (use_mf) {
-        Q3VL_HIP(launch_quantize_frag(A, aq, asT, (int)M, (int)K, st), "quantize launch");
         const int Mt = (int)((M + 31) / 32);
+        // 5..16 rows against a very wide weight (the lm_head over a batch of
+        // rows): 16-row MFMA tiles with the weights loaded straight into the
+        // operands, the activations quantized inside the kernel
+        bool wide16 = Mt == 1 && M >= 5 && mode != GEMV_SWIGLU;
+        for (int i = 0; wide16 && i < nseg; ++i)
+            wide16 = (size_t)Ns[i] * K >= ((size_t)1 << 26) &&
+                     gemm_mf_wide_serves((int)M, (int)Ns[i], (int)K);
+        if (wide16) {
+            for (int i = 0; i < nseg; ++i) {
+                float *pv = nullptr;
+                int32_t *pi = nullptr;
+                int nparts = 0;
+                if (mode == GEMV_ARGMAX) {
+                    pv = reinterpret_cast<float *>(wbase + LG.parts_val);
+                    pi = reinterpret_cast<int32_t *>(wbase + LG.parts_idx);
+                    nparts = gemm_mf_wide_parts((int)Ns[i], cus);
+                    if ((size_t)nparts > kMaxGemvParts) return Q3VL_ERR_UNSUPPORTED;
+                }
+                Q3VL_HIP(launch_gemm_mf_wide(A, W[i], S[i], C[i], (int)M, (int)Ns[i], (int)K, pv, pi, cus, st),
+                         "wide gemm launch");
+                if (mode == GEMV_ARGMAX)
+                    Q3VL_HIP(launch_argmax_final(pv, pi, nparts, (int)M, ids, st), "argmax launch");
+            }
+            return Q3VL_OK;
+        }
+        Q3VL_HIP(launch_quantize_frag(A, aq, asT, (int)M, (int)K, st), "quantize launch");
         if (mode == GEMV_SWIGLU) {
             GemmMfArgs g{aq, asT, Mt, W[0], S[0], W[1], S[1], C[0], (int)M, (int)Ns[0], (int)K};
             Q3VL_HIP(launch_gemm_mf(g, true, cus, st), "gemm launch");

@@ -58,6 +58,7 @@ namespace q3vl {
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef float float16_t __attribute__((ext_vector_type(16)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // ---------------------------------------------------- fragment-order quantizer
@@ -729,6 +730,281 @@ hipError_t launch_gemm_mf(const GemmMfArgs &a, bool swiglu, int cus, hipStream_t
     }
     if (a.Mt == 1) return launch_mf<1, 1, false, 2, 3, 1, true, 8>(a, st);
     return launch_mf<1, 1, false, 2, 4, 2, false, 8>(a, st);
+}
+
+// ------------------------------------------------ wide products, few rows
+// 16 or fewer activation rows against a very wide weight (the lm_head over a
+// batch of rows): the product is 16 rows x N, so the 32-row tiles above would
+// pad it, and they stage every weight row through LDS. Here one wave computes
+// 16 weight rows x the 16 activation rows with v_mfma_f32_16x16x32_f16, the
+// weights going straight from the load into the MFMA operand:
+// * B (weights): lane l takes weight row n = l % 16 of the tile and, of each
+//   group's 64 bytes, bytes 16c .. 16c + 15 (c = l / 16) -- one 16-byte load a
+//   lane and group; widened to fp16 (0x64xx trick), its first 8 k feed the
+//   group's first MFMA, the other 8 the second.
+// * A: MFMA u of lane l takes row l % 16, k = 16c + 8u + j (j = 0..7) -- the k
+//   the weight bytes hold. Each block quantizes the activations itself into
+//   LDS in that lane order, 16-byte pieces [group][u][lane], and the a_s as
+//   [group][row] (rows M..15 zero), so no quantizer launch precedes it: a
+//   team of 4 lanes per (row, group) runs the reference quantizer
+//   (i8:135-177) in its own order -- the 16 FMA chains over x[16t + i]^2,
+//   P0[i] + P1[i], the fixed tree, s = sqrt(sumsq/64 + 1e-6) / 127 as
+//   quantize_frag_kernel's group_scale, q = rne(x * (1/s)) saturated to
+//   int16, as fp16 (exact: |q| <= 1016 wherever s is finite).
+// * G of a group is the MFMA pair's exact integer sum (as in gemm_mf_kernel);
+//   lane l holds rows 4c + i, column n, and folds out = fma(G * a_s, w_s, out)
+//   group by group in ascending order (i8:613-617, 652).
+// * Wave w takes tiles [w tpw, (w+1) tpw) of 16 weight rows; its loads run
+//   D quads (4 groups each) ahead, across its tiles. Per tile it keeps the
+//   greedy-argmax candidate of each row (am_combine over its columns; values
+//   not above -FLT_MAX never win), and at the end leaves one partial per row.
+template <int D, int MINB = 2>
+__global__ __launch_bounds__(256, MINB) void gemm_mf_wide_kernel(const float *A,
+                                                              const int8_t *W, const float *S, int N,
+                                                              int K, int M, int tpw, int ntiles,
+                                                              float *C, float *part_val,
+                                                              int32_t *part_idx) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int Kg = K / 64, qpt = Kg / 4;  // groups; quads per tile
+    u32x4 *Al = reinterpret_cast<u32x4 *>(smem);                  // [Kg][2][64]
+    float *asl = reinterpret_cast<float *>(smem + Kg * 2 * 64 * 16);  // [Kg][16]
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int gw = (int)blockIdx.x * 4 + wid;  // this wave's partial
+    const int t0 = gw * tpw, t1 = min(t0 + tpw, ntiles);
+
+    constexpr int kRsrcWord3 = 0x00020000;
+    const __amdgpu_buffer_rsrc_t rW = __builtin_amdgcn_make_buffer_rsrc((void *)W, 0, N * K, kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t rS = __builtin_amdgcn_make_buffer_rsrc((void *)S, 0, N * Kg * 4, kRsrcWord3);
+    const int c = lane >> 4, nl = lane & 15;
+    // weight row of tile t (clamped into the weight; columns past N are not
+    // kept) and its byte offset of quad q
+    u32x4 wr[D][4];
+    float4 wsr[D];
+    const int nq = max(t1 - t0, 0) * qpt;  // quads over the wave's tiles
+    auto load = [&](int sl, int Q) __attribute__((always_inline)) {
+        const int t = t0 + Q / qpt, g0 = 4 * (Q % qpt);
+        const int row = min(16 * t + nl, N - 1);
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            wr[sl][u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                      rW, row * K + 16 * c, 64 * (g0 + u), 0));
+        wsr[sl] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rS, row * Kg * 4, 4 * g0, 0));
+    };
+    // the weight stream starts before the activations are quantized; the
+    // slots are issued in ring order, as the loop reissues them (the wait
+    // counts at the loop head cover both paths: any other order here would
+    // make every quad's first use wait for nearly every load in flight)
+    if (nq > 0) {
+#pragma unroll
+        for (int j = 0; j < D; ++j) {
+            __builtin_amdgcn_sched_barrier(0);
+            load(j, min(j, nq - 1));
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    // ---- quantize A into LDS (every thread of the block, before its
+    // barrier). A team of 4 lanes per (row, group), rows 0..RW-1, groups
+    // fastest (a wave's loads read 16 consecutive 256-byte groups, 64 bytes
+    // a team each); rows past M are zeros, and with RW = 8 rows 8..15 are
+    // zero-filled. Lane j of a team holds x[16v + 4j + c] (v, c = 0..3):
+    // the whole chains i = 4j + c of the sum of squares, t = v ascending.
+    // v_i = P_i + P_{i+8} pairs lanes j and j + 2, the tree's v_i + v_{i+4}
+    // lanes 0 and 1, then (s0 + s1) + (s2 + s3) in lane 0.
+    const int RW = M <= 8 ? 8 : 16;
+    if (RW == 8) {
+        for (int q = tid; q < Kg * 16; q += 256) {  // (group, u, c) pieces of rows 8..15
+            const int g = q >> 4, u = (q >> 3) & 1, cc = (q >> 1) & 3, r = 8 + 4 * (q & 1);
+            u32x4 *d = Al + (g * 2 + u) * 64 + 16 * cc + r;
+#pragma unroll
+            for (int z = 0; z < 4; ++z) d[z] = (u32x4){0u, 0u, 0u, 0u};
+        }
+        for (int q = tid; q < Kg * 8; q += 256) asl[(q >> 3) * 16 + 8 + (q & 7)] = 0.0f;
+    }
+    const int tj = tid & 3;
+    for (int tm = tid >> 2; tm < RW * Kg; tm += 64) {
+        const int g = tm % Kg, m = tm / Kg;
+        const bool real = m < M;
+        float4 xv[4];
+        const float *xr = A + (size_t)min(m, M - 1) * K + 64 * g + 4 * tj;
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+            xv[v] = real ? *reinterpret_cast<const float4 *>(xr + 16 * v) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        float P[4];
+        P[0] = fmaf(xv[0].x, xv[0].x, 0.0f);
+        P[1] = fmaf(xv[0].y, xv[0].y, 0.0f);
+        P[2] = fmaf(xv[0].z, xv[0].z, 0.0f);
+        P[3] = fmaf(xv[0].w, xv[0].w, 0.0f);
+#pragma unroll
+        for (int v = 1; v < 4; ++v) {
+            P[0] = fmaf(xv[v].x, xv[v].x, P[0]);
+            P[1] = fmaf(xv[v].y, xv[v].y, P[1]);
+            P[2] = fmaf(xv[v].z, xv[v].z, P[2]);
+            P[3] = fmaf(xv[v].w, xv[v].w, P[3]);
+        }
+        float V[4], T[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) V[c] = P[c] + __shfl_xor(P[c], 2, 4);  // lanes 0, 1: v_{4j+c}
+#pragma unroll
+        for (int c = 0; c < 4; ++c) T[c] = V[c] + __shfl_xor(V[c], 1, 4);  // lane 0: s_c
+        const float sumsq = __shfl((T[0] + T[1]) + (T[2] + T[3]), 0, 4);
+        const float sc = group_scale(sumsq, 1.0f / 64.0f);
+        const float inv = rcp_rn(sc);
+        // q = rne(x * inv): for a finite scale |q| <= 1016, and adding and
+        // removing 1.5 * 2^23 rounds to the integer, ties to even, exactly
+        // in fp16 (quant_pair_finite's integer); otherwise the saturating
+        // conversion of the reference, as int16 converted to fp16
+        uint32_t h[8];  // h[2v + e]: elements 16v + 4tj + 2e, +1
+        if (__builtin_expect(__builtin_isfinite(sc), 1)) {
+            constexpr float kMagic = 12582912.0f;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const float r0 = (xv[v].x * inv + kMagic) - kMagic, r1 = (xv[v].y * inv + kMagic) - kMagic;
+                const float r2 = (xv[v].z * inv + kMagic) - kMagic, r3 = (xv[v].w * inv + kMagic) - kMagic;
+                h[2 * v] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(r0, r1));
+                h[2 * v + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(r2, r3));
+            }
+        } else {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const uint32_t q0 = quant_pair(xv[v].x * inv, xv[v].y * inv);
+                const uint32_t q1 = quant_pair(xv[v].z * inv, xv[v].w * inv);
+                h[2 * v] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(
+                                                  (float)(int16_t)(q0 & 0xFFFF), (float)(int16_t)(q0 >> 16)));
+                h[2 * v + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(
+                                                      (float)(int16_t)(q1 & 0xFFFF), (float)(int16_t)(q1 >> 16)));
+            }
+        }
+        // elements 16v + 4tj + c are halves 4(tj % 2) + c of piece 2v + tj / 2,
+        // i.e. (u, lane c') = (tj / 2, 16v + m)
+        unsigned char *Ab = reinterpret_cast<unsigned char *>(Al);
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+            *reinterpret_cast<uint2 *>(Ab + ((g * 2 + (tj >> 1)) * 64 + 16 * v + m) * 16 + 8 * (tj & 1)) =
+                real ? make_uint2(h[2 * v], h[2 * v + 1]) : make_uint2(0u, 0u);
+        if (tj == 0) asl[g * 16 + m] = real ? sc : 0.0f;
+    }
+    __syncthreads();
+    if (nq == 0) return;  // no tile for this wave (no barrier follows)
+
+    float4 out = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    float bv[4] = {-FLT_MAX, -FLT_MAX, -FLT_MAX, -FLT_MAX};
+    int32_t bi[4] = {-1, -1, -1, -1};
+    auto step = [&](int sl, int Q) __attribute__((always_inline)) {
+        const int g0 = 4 * (Q % qpt);
+        half8_t bf[4][2];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const u32x4 v = wr[sl][u] ^ (u32x4){0x80808080u, 0x80808080u, 0x80808080u, 0x80808080u};
+            uint32_t w[8];
+            widen4_mf(v.x, w[0], w[1]);
+            widen4_mf(v.y, w[2], w[3]);
+            widen4_mf(v.z, w[4], w[5]);
+            widen4_mf(v.w, w[6], w[7]);
+            bf[u][0] = __builtin_bit_cast(half8_t, (u32x4){w[0], w[1], w[2], w[3]});
+            bf[u][1] = __builtin_bit_cast(half8_t, (u32x4){w[4], w[5], w[6], w[7]});
+        }
+        // the scales copied out by real moves: kept as the slot's registers,
+        // they would be live across the reload, which then takes other
+        // registers and the loop's back edge copies them after a wait for
+        // every load in flight
+        float ws[4];
+        asm volatile("v_mov_b32 %0, %1" : "=v"(ws[0]) : "v"(wsr[sl].x));
+        asm volatile("v_mov_b32 %0, %1" : "=v"(ws[1]) : "v"(wsr[sl].y));
+        asm volatile("v_mov_b32 %0, %1" : "=v"(ws[2]) : "v"(wsr[sl].z));
+        asm volatile("v_mov_b32 %0, %1" : "=v"(ws[3]) : "v"(wsr[sl].w));
+        // the slot's reload goes out here, after its values are consumed and
+        // before this quad's MFMAs (pinned: left to itself, the scheduler
+        // hoists reloads into fresh registers ahead of earlier uses, and the
+        // ring's loads then retire in an order that makes each use wait for
+        // nearly every load in flight)
+        __builtin_amdgcn_sched_barrier(0);
+        load(sl, min(Q + D, nq - 1));  // (past the last quad: the last again)
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int g = g0 + u;
+            const half8_t a0 = __builtin_bit_cast(half8_t, Al[(g * 2 + 0) * 64 + lane]);
+            const half8_t a1 = __builtin_bit_cast(half8_t, Al[(g * 2 + 1) * 64 + lane]);
+            const float4 as4 = *reinterpret_cast<const float4 *>(asl + g * 16 + 4 * c);
+            float4_t acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, bf[u][0], (float4_t){0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, bf[u][1], acc, 0, 0, 0);
+            out.x = fmaf(acc[0] * as4.x, ws[u], out.x);
+            out.y = fmaf(acc[1] * as4.y, ws[u], out.y);
+            out.z = fmaf(acc[2] * as4.z, ws[u], out.z);
+            out.w = fmaf(acc[3] * as4.w, ws[u], out.w);
+        }
+        if (Q % qpt == qpt - 1) {  // uniform: the tile's last quad
+            const int col = 16 * (t0 + Q / qpt) + nl;
+            const float o4[4] = {out.x, out.y, out.z, out.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int row = 4 * c + i;
+                if (row < M && col < N) {
+                    if (C) C[(size_t)row * N + col] = o4[i];
+                    if (o4[i] > -FLT_MAX) am_combine(bv[i], bi[i], o4[i], col);
+                }
+            }
+            out = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+    };
+    // nq is a multiple of D (D divides the quads of a tile): whole ring turns
+    for (int Q0 = 0; Q0 < nq; Q0 += D) {
+#pragma unroll
+        for (int j = 0; j < D; ++j) step(j, Q0 + j);
+    }
+    // ---- the wave's partial per row: the 16 lanes of row group c
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int off = 8; off > 0; off >>= 1) {
+            const float ov = __shfl_xor(bv[i], off);
+            const int32_t oi = __shfl_xor(bi[i], off);
+            am_combine(bv[i], bi[i], ov, oi);
+        }
+        const int row = 4 * c + i;
+        if (part_val && nl == 0 && row < M) {
+            part_val[(size_t)gw * M + row] = bv[i];
+            part_idx[(size_t)gw * M + row] = bi[i];
+        }
+    }
+}
+
+constexpr int kWideD = 2;  // quads in flight per wave of gemm_mf_wide_kernel
+
+bool gemm_mf_wide_serves(int M, int N, int K) {
+    // K: whole quads of groups, the ring's D quads dividing a tile's, and the
+    // block's A fragments (32 K bytes) within half of a CU's LDS
+    return M >= 1 && M <= 16 && N >= 16 && K > 0 && K % (256 * kWideD) == 0 && K <= 2048;
+}
+
+// Tiles of 16 weight rows per wave: enough waves for two 4-wave blocks per CU.
+static int wide_tpw(int N, int cus) {
+    const int ntiles = (N + 15) / 16;
+    const int waves = 8 * max(cus, 1);
+    return (ntiles + waves - 1) / waves;
+}
+
+int gemm_mf_wide_parts(int N, int cus) {
+    const int ntiles = (N + 15) / 16, tpw = wide_tpw(N, cus);
+    return (ntiles + tpw - 1) / tpw;
+}
+
+hipError_t launch_gemm_mf_wide(const float *A, const int8_t *W, const float *S, float *C, int M, int N,
+                               int K, float *part_val, int32_t *part_idx, int cus, hipStream_t st) {
+    if (!gemm_mf_wide_serves(M, N, K) || (size_t)N * K > 0x7fffffffULL || (!part_val) != (!part_idx) ||
+        (!C && !part_val))
+        return hipErrorInvalidValue;
+    const int ntiles = (N + 15) / 16, tpw = wide_tpw(N, cus);
+    const int waves = (ntiles + tpw - 1) / tpw;
+    const size_t lds = (size_t)(K / 64) * (2 * 64 * 16 + 16 * 4);
+    static const hipError_t attr = hipFuncSetAttribute(
+        reinterpret_cast<const void *>(&gemm_mf_wide_kernel<kWideD>), hipFuncAttributeMaxDynamicSharedMemorySize,
+        (int)((2048 / 64) * (2 * 64 * 16 + 16 * 4)));
+    if (attr != hipSuccess) return attr;
+    gemm_mf_wide_kernel<kWideD><<<(waves + 3) / 4, 256, lds, st>>>(A, W, S, N, K, M, tpw, ntiles, C, part_val,
+                                                                    part_idx);
+    return hipGetLastError();
 }
 
 }  // namespace q3vl

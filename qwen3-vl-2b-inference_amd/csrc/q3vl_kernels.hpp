@@ -151,5 +151,14 @@ hipError_t launch_quantize_frag(const float *A, _Float16 *qf, float *asf, int M,
 // launch_gemm's kernels, with launch_quantize_f16), on a device of `cus` CUs.
 bool gemm_mf_serves(int M, int N, int K, bool swiglu, int cus);
 hipError_t launch_gemm_mf(const GemmMfArgs &a, bool swiglu, int cus, hipStream_t st);
+// 16 or fewer rows of fp32 activations A [M, K] against a wide weight (K %
+// 512 == 0, K <= 2048): quantized inside the kernel, 16 x 16 MFMA tiles with
+// the weights loaded straight into the operands. With argmax partial buffers
+// it leaves gemm_mf_wide_parts(N, cus) partials per row, [parts][M]; C may
+// then be null.
+bool gemm_mf_wide_serves(int M, int N, int K);
+int gemm_mf_wide_parts(int N, int cus);
+hipError_t launch_gemm_mf_wide(const float *A, const int8_t *W, const float *S, float *C, int M, int N,
+                               int K, float *part_val, int32_t *part_idx, int cus, hipStream_t st);
 
 }  // namespace q3vl

@@ -147,7 +147,8 @@ def test_gemm_parity(orc, M, N, K, gs):
                                    (784, 1024, 4096), (196, 4096, 4096)])
 def test_gemm_group64_tiles_parity(orc, M, N, K):
     """The group-64 MFMA GEMMs: the fragment-order kernel (K a multiple of
-    512) with one m-tile (32 x 128 tiles) or several (64 x 64 tiles), a
+    512) with one m-tile (32 x 128 tiles; 7 rows against the 65600-row
+    weight take the 16-row wide kernel) or several (64 x 64 tiles), a
     single w_s tile (K = 512) and an odd number of them (K = 1536), and the
     row-major kernel for the other K; ragged M and N, bit-exact. Every
     vision-encoder linear at its own shape: qkv (784, 3072, 1024), proj
@@ -380,9 +381,9 @@ def test_lm_head_argmax_lane_ties_across_tiles(orc, V, off):
                                    (20, 40000, 2048), (32, 33000, 2048)])
 def test_lm_head_argmax_gemm_path(orc, M, V, K):
     """lm_head + argmax on the GEMM (then the row argmax): M > 8, and 5..8
-    rows against a very wide weight; one m-tile (M <= 32) takes the 1 x 4
-    wave tiles. A planted tie that the lowest index must win, logits
-    bit-exact."""
+    rows against a very wide weight (6 x 70001: the 16-row wide kernel);
+    the other single m-tile shapes (M <= 32) take the 1 x 4 wave tiles. A
+    planted tie that the lowest index must win, logits bit-exact."""
     gs = 64
     A, W, S = make_case(77 + M, M, V, K, gs)
     top = int(orc.argmax_rows(orc.linear(A[:1], W, S, gs))[0])
@@ -396,6 +397,57 @@ def test_lm_head_argmax_gemm_path(orc, M, V, K):
     ids = host(q.lm_head_argmax(dev(A), dev(W), dev(S), gs, logits=logits))
     assert_bits_equal(host(logits), logits_ref, "logits")
     np.testing.assert_array_equal(ids, ids_ref)
+
+
+@pytest.mark.parametrize("M,V,K", [(16, 40007, 2048), (13, 65541, 1024), (5, 33000, 2048)])
+def test_lm_head_argmax_wide_rows(orc, M, V, K):
+    """5..16 rows against a very wide weight (V * K >= 2^26, K <= 2048): the
+    16-row MFMA tiles with the weights loaded straight into the operands, one
+    argmax partial per wave. V = 40007 and 65541 leave a last tile of 7 and 5
+    valid rows. First row 0's winner copied to a column about 2000 lower
+    (another wave's tiles) and next to itself: the lowest index must win.
+    Then a row of NaN activations (id 0), a column made +-inf/NaN by an
+    infinite weight scale and a column of -inf logits for one row. Logits
+    bit-exact, ids with and without them stored."""
+    gs = 64
+    A, W, S = make_case(9100 + M, M, V, K, gs)
+
+    def check(A, W, S):
+        logits_ref = orc.linear(A, W, S, gs)
+        ids_ref = orc.argmax_rows(logits_ref)
+        logits = torch.empty((M, V), dtype=torch.float32, device="cuda")
+        ids = host(q.lm_head_argmax(dev(A), dev(W), dev(S), gs, logits=logits))
+        np.testing.assert_array_equal(ids, ids_ref)
+        got = host(logits)
+        nan = np.isnan(logits_ref)
+        assert np.array_equal(np.isnan(got), nan)
+        np.testing.assert_array_equal(got[~nan].view(np.uint32), logits_ref[~nan].view(np.uint32))
+        np.testing.assert_array_equal(host(q.lm_head_argmax(dev(A), dev(W), dev(S), gs)), ids_ref)
+        return logits_ref, ids_ref
+
+    top = int(orc.argmax_rows(orc.linear(A[:1], W, S, gs))[0])
+    lo = top - 2000 if top >= 2000 else top + 2500
+    for r in (lo, min(top + 1, V - 1)):
+        W[r] = W[top]
+        S[r] = S[top]
+    logits_ref, ids_ref = check(A, W, S)
+    assert logits_ref[0, lo] == logits_ref[0, top] and ids_ref[0] == min(lo, top)
+
+    A[M - 1, :] = np.nan
+    S[17, 3] = np.inf
+    W[33, :] = -127
+    S[33, :] = np.float32(3e38)
+    A[2, :] = np.abs(A[2, :]) + 0.5  # row 2: column 33 -> -inf
+    logits_ref, ids_ref = check(A, W, S)
+    assert ids_ref[M - 1] == 0 and np.isneginf(logits_ref[2, 33])
+
+
+def test_linear_wide_rows(orc):
+    """The 16-row tiles as a plain product (outputs only, no argmax): M = 9
+    against a 36000 x 2048 weight."""
+    M, N, K, gs = 9, 36000, 2048, 64
+    A, W, S = make_case(9200, M, N, K, gs)
+    assert_bits_equal(host(q.linear_i8(dev(A), dev(W), dev(S), gs)), orc.linear(A, W, S, gs), "C")
 
 
 def test_lm_head_argmax_partials_over_passes(orc):
