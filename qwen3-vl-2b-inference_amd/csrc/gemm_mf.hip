@@ -754,24 +754,27 @@ hipError_t launch_gemm_mf(const GemmMfArgs &a, bool swiglu, int cus, hipStream_t
 // * G of a group is the MFMA pair's exact integer sum (as in gemm_mf_kernel);
 //   lane l holds rows 4c + i, column n, and folds out = fma(G * a_s, w_s, out)
 //   group by group in ascending order (i8:613-617, 652).
-// * Wave w takes tiles [w tpw, (w+1) tpw) of 16 weight rows; its loads run
-//   D quads (4 groups each) ahead, across its tiles. Per tile it keeps the
-//   greedy-argmax candidate of each row (am_combine over its columns; values
-//   not above -FLT_MAX never win), and at the end leaves one partial per row.
-template <int D, int MINB = 2>
-__global__ __launch_bounds__(256, MINB) void gemm_mf_wide_kernel(const float *A,
-                                                              const int8_t *W, const float *S, int N,
-                                                              int K, int M, int tpw, int ntiles,
-                                                              float *C, float *part_val,
-                                                              int32_t *part_idx) {
+// * Each wave takes a contiguous run of 16-row tiles (the runs differ by at
+//   most one tile); its loads run D quads (4 groups each) ahead, across its
+//   tiles. Per tile it keeps the greedy-argmax candidate of each row
+//   (am_combine over its columns; values not above -FLT_MAX never win), and
+//   at the end leaves one partial per row (an empty one without tiles).
+template <int D, int NW, int MINB>
+__global__ __launch_bounds__(64 * NW, MINB) void gemm_mf_wide_kernel(const float *A,
+                                                                 const int8_t *W, const float *S, int N,
+                                                                 int K, int M, int nwaves, int ntiles,
+                                                                 float *C, float *part_val,
+                                                                 int32_t *part_idx) {
+    constexpr int NT = 64 * NW;  // threads
     extern __shared__ __align__(16) unsigned char smem[];
     const int Kg = K / 64, qpt = Kg / 4;  // groups; quads per tile
     u32x4 *Al = reinterpret_cast<u32x4 *>(smem);                  // [Kg][2][64]
     float *asl = reinterpret_cast<float *>(smem + Kg * 2 * 64 * 16);  // [Kg][16]
     const int tid = threadIdx.x, lane = tid & 63;
     const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int gw = (int)blockIdx.x * 4 + wid;  // this wave's partial
-    const int t0 = gw * tpw, t1 = min(t0 + tpw, ntiles);
+    const int gw = (int)blockIdx.x * NW + wid;  // this wave's partial
+    // tiles [t0, t1): the waves' shares differ by at most one tile
+    const int t0 = (int)((long)gw * ntiles / nwaves), t1 = (int)((long)(gw + 1) * ntiles / nwaves);
 
     constexpr int kRsrcWord3 = 0x00020000;
     const __amdgpu_buffer_rsrc_t rW = __builtin_amdgcn_make_buffer_rsrc((void *)W, 0, N * K, kRsrcWord3);
@@ -813,16 +816,16 @@ __global__ __launch_bounds__(256, MINB) void gemm_mf_wide_kernel(const float *A,
     // lanes 0 and 1, then (s0 + s1) + (s2 + s3) in lane 0.
     const int RW = M <= 8 ? 8 : 16;
     if (RW == 8) {
-        for (int q = tid; q < Kg * 16; q += 256) {  // (group, u, c) pieces of rows 8..15
+        for (int q = tid; q < Kg * 16; q += NT) {  // (group, u, c) pieces of rows 8..15
             const int g = q >> 4, u = (q >> 3) & 1, cc = (q >> 1) & 3, r = 8 + 4 * (q & 1);
             u32x4 *d = Al + (g * 2 + u) * 64 + 16 * cc + r;
 #pragma unroll
             for (int z = 0; z < 4; ++z) d[z] = (u32x4){0u, 0u, 0u, 0u};
         }
-        for (int q = tid; q < Kg * 8; q += 256) asl[(q >> 3) * 16 + 8 + (q & 7)] = 0.0f;
+        for (int q = tid; q < Kg * 8; q += NT) asl[(q >> 3) * 16 + 8 + (q & 7)] = 0.0f;
     }
     const int tj = tid & 3;
-    for (int tm = tid >> 2; tm < RW * Kg; tm += 64) {
+    for (int tm = tid >> 2; tm < RW * Kg; tm += NT / 4) {
         const int g = tm % Kg, m = tm / Kg;
         const bool real = m < M;
         float4 xv[4];
@@ -885,7 +888,17 @@ __global__ __launch_bounds__(256, MINB) void gemm_mf_wide_kernel(const float *A,
         if (tj == 0) asl[g * 16 + m] = real ? sc : 0.0f;
     }
     __syncthreads();
-    if (nq == 0) return;  // no tile for this wave (no barrier follows)
+    if (nq == 0) {  // no tile for this wave: an empty partial (no barrier follows)
+        if (part_val && (lane & 15) == 0) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                if (4 * (lane >> 4) + i < M) {
+                    part_val[(size_t)gw * M + 4 * (lane >> 4) + i] = -FLT_MAX;
+                    part_idx[(size_t)gw * M + 4 * (lane >> 4) + i] = -1;
+                }
+        }
+        return;
+    }
 
     float4 out = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     float bv[4] = {-FLT_MAX, -FLT_MAX, -FLT_MAX, -FLT_MAX};
@@ -970,7 +983,9 @@ __global__ __launch_bounds__(256, MINB) void gemm_mf_wide_kernel(const float *A,
     }
 }
 
-constexpr int kWideD = 2;  // quads in flight per wave of gemm_mf_wide_kernel
+constexpr int kWideD = 2;   // quads in flight per wave of gemm_mf_wide_kernel
+constexpr int kWideNW = 4;  // waves per block
+constexpr int kWideBPC = 1; // blocks per CU
 
 bool gemm_mf_wide_serves(int M, int N, int K) {
     // K: whole quads of groups, the ring's D quads dividing a tile's, and the
@@ -978,16 +993,14 @@ bool gemm_mf_wide_serves(int M, int N, int K) {
     return M >= 1 && M <= 16 && N >= 16 && K > 0 && K % (256 * kWideD) == 0 && K <= 2048;
 }
 
-// Tiles of 16 weight rows per wave: enough waves for two 4-wave blocks per CU.
-static int wide_tpw(int N, int cus) {
-    const int ntiles = (N + 15) / 16;
-    const int waves = 8 * max(cus, 1);
-    return (ntiles + waves - 1) / waves;
-}
-
+// Waves: kWideBPC blocks of kWideNW waves per CU, fewer where the weight has
+// fewer 16-row tiles; one argmax partial each. (Fewer, longer waves measured
+// faster than two blocks per CU: the blocks' prologue quantizers repeat the
+// same work.)
 int gemm_mf_wide_parts(int N, int cus) {
-    const int ntiles = (N + 15) / 16, tpw = wide_tpw(N, cus);
-    return (ntiles + tpw - 1) / tpw;
+    const int ntiles = (N + 15) / 16;
+    const int blocks = min(kWideBPC * max(cus, 1), (ntiles + kWideNW - 1) / kWideNW);
+    return blocks * kWideNW;
 }
 
 hipError_t launch_gemm_mf_wide(const float *A, const int8_t *W, const float *S, float *C, int M, int N,
@@ -995,15 +1008,14 @@ hipError_t launch_gemm_mf_wide(const float *A, const int8_t *W, const float *S, 
     if (!gemm_mf_wide_serves(M, N, K) || (size_t)N * K > 0x7fffffffULL || (!part_val) != (!part_idx) ||
         (!C && !part_val))
         return hipErrorInvalidValue;
-    const int ntiles = (N + 15) / 16, tpw = wide_tpw(N, cus);
-    const int waves = (ntiles + tpw - 1) / tpw;
+    const int ntiles = (N + 15) / 16, nwaves = gemm_mf_wide_parts(N, cus);
     const size_t lds = (size_t)(K / 64) * (2 * 64 * 16 + 16 * 4);
     static const hipError_t attr = hipFuncSetAttribute(
-        reinterpret_cast<const void *>(&gemm_mf_wide_kernel<kWideD>), hipFuncAttributeMaxDynamicSharedMemorySize,
-        (int)((2048 / 64) * (2 * 64 * 16 + 16 * 4)));
+        reinterpret_cast<const void *>(&gemm_mf_wide_kernel<kWideD, kWideNW, 2>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, (int)((2048 / 64) * (2 * 64 * 16 + 16 * 4)));
     if (attr != hipSuccess) return attr;
-    gemm_mf_wide_kernel<kWideD><<<(waves + 3) / 4, 256, lds, st>>>(A, W, S, N, K, M, tpw, ntiles, C, part_val,
-                                                                    part_idx);
+    gemm_mf_wide_kernel<kWideD, kWideNW, 2><<<nwaves / kWideNW, 64 * kWideNW, lds, st>>>(
+        A, W, S, N, K, M, nwaves, ntiles, C, part_val, part_idx);
     return hipGetLastError();
 }
 
