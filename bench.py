@@ -869,6 +869,67 @@ def pmc_workload_gemm():
         log(f"pmc gemm workload: {name} {M}x{N}x{K} done")
 
 
+def pmc_workload_lmhead():
+    """Workload for the lm_head traffic passes: the calibration copy of
+    pmc_workload, then 3 calls each of config 3's lm_head + argmax at M = 1
+    (gemv_kernel) and M = 8 (gemm_mf_wide_kernel), every call on its own
+    weight copy (3 x 331 MB: each streams from HBM)."""
+    import torch
+    import q3vl_int8 as q
+    n = 256 << 20
+    src = torch.ones(n, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    torch.add(src, 1, out=dst)
+    torch.cuda.synchronize()
+    del src, dst
+    V, K = 151936, 2048
+    Ws, Ss = gen_weights(V, K, 3, 0xC0FFEE03)
+    for M in (1, 8):
+        x = torch.randn((M, K), dtype=torch.float32, device="cuda")
+        ids = torch.empty((M,), dtype=torch.int32, device="cuda")
+        ws = q.alloc_workspace(M, V, K, GS)
+        for i in range(3):
+            q.lm_head_argmax(x, Ws[i], Ss[i], GS, ids=ids, workspace=ws)
+        torch.cuda.synchronize()
+    log("pmc lm_head workload done")
+
+
+def pmc_kernel_traffic(fetch_dir, write_dir):
+    """HBM bytes per dispatch of every kernel in two rocprofv3 --pmc runs of
+    a counter workload (FETCH_SIZE, then WRITE_SIZE), each counter scaled by
+    what it reads for the workload's calibration copy (256 MiB read, 256 MiB
+    written), as pmc_traffic scales the decode GEMVs'."""
+    import csv
+    import glob
+
+    def per_kernel(d, counter):
+        rows = {}
+        for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            with open(f, newline="") as fh:
+                for r in csv.DictReader(fh):
+                    if r["Counter_Name"] == counter:
+                        rows.setdefault(r.get("Kernel_Name", ""), []).append(float(r["Counter_Value"]))
+        return rows
+
+    fetch, write = per_kernel(fetch_dir, "FETCH_SIZE"), per_kernel(write_dir, "WRITE_SIZE")
+    cands = [(max(v), k) for k, v in fetch.items() if "elementwise" in k]
+    if not cands:
+        raise SystemExit("no calibration (elementwise) dispatch in the FETCH_SIZE run")
+    n_cal = 256 << 20
+    ff = n_cal / (max(cands)[0] * 1024)
+    wf = n_cal / (max(max(v) for k, v in write.items() if "elementwise" in k) * 1024)
+    out = {"calibration": {"fetch_factor": round(ff, 4), "write_factor": round(wf, 4)}}
+    for k in sorted(fetch):
+        if "elementwise" in k or "distribution" in k:
+            continue
+        fk = sum(fetch[k]) / len(fetch[k])
+        w = write.get(k, [0.0])
+        out[k[:120]] = {"dispatches": len(fetch[k]), "fetch_bytes": round(fk * 1024 * ff),
+                        "write_bytes": round(sum(w) / len(w) * 1024 * wf)}
+    return out
+
+
 def pmc_summary(dirs, match):
     """Average counter values per dispatch for the kernels whose name holds
     `match`, from rocprofv3 --pmc runs (counter_collection.csv under each
@@ -1074,9 +1135,13 @@ def main():
     ap.add_argument("--pmc-traffic", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="print the decode GEMVs' HBM traffic summary from the FETCH_SIZE and "
                          "WRITE_SIZE runs of --pmc-workload")
-    ap.add_argument("--pmc-workload", nargs="?", const="decode", choices=["decode", "gemm"],
+    ap.add_argument("--pmc-workload", nargs="?", const="decode", choices=["decode", "gemm", "lmhead"],
                     help="run only the workload of the counter passes: decode (the decode "
-                         "GEMVs' HBM traffic, the default) or gemm (configs 2 and 4's GEMMs)")
+                         "GEMVs' HBM traffic, the default), gemm (configs 2 and 4's GEMMs) or "
+                         "lmhead (config 3's lm_head at M = 1 and 8)")
+    ap.add_argument("--pmc-kernel-traffic", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="print every kernel's HBM bytes per dispatch from the FETCH_SIZE and "
+                         "WRITE_SIZE runs of a --pmc-workload")
     ap.add_argument("--trace-summary", metavar="KERNEL_TRACE_CSV",
                     help="summarize a rocprofv3 kernel trace of this bench and exit")
     args = ap.parse_args()
@@ -1088,6 +1153,9 @@ def main():
         return
     if args.pmc_traffic:
         print(json.dumps(pmc_traffic(*args.pmc_traffic), indent=1))
+        return
+    if args.pmc_kernel_traffic:
+        print(json.dumps(pmc_kernel_traffic(*args.pmc_kernel_traffic), indent=1))
         return
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (see the sharding "
@@ -1104,7 +1172,7 @@ def main():
     q.lib()  # fails loudly if the HIP library is missing
     torch.cuda.set_device(0)
     if args.pmc_workload:
-        pmc_workload_gemm() if args.pmc_workload == "gemm" else pmc_workload()
+        {"gemm": pmc_workload_gemm, "lmhead": pmc_workload_lmhead}.get(args.pmc_workload, pmc_workload)()
         return
     configs = args.configs.split(",")
     dims = decode_dims(max_seq=(CTX + args.warmup + args.steps + 7 + 15) // 8 * 8)
