@@ -198,8 +198,8 @@ int run_linear(const float *A, int nseg, const int8_t *const *W, const float *co
     if (rc) return rc;
 
     // 5..8 rows against a very wide weight (the lm_head over a batch of
-    // rows): the MFMA GEMM, with the rows padded to one 32-row tile, streams
-    // the weights faster than the general GEMV's integer dot products.
+    // rows): the MFMA kernels below (16-row tiles, see wide16) stream the
+    // weights faster than the general GEMV's integer dot products.
     bool wide_mf = M >= 5 && M <= 8 && gs == 64 && mode != GEMV_SWIGLU;
     for (int i = 0; wide_mf && i < nseg; ++i)
         wide_mf = !(G && G[i]) && (size_t)Ns[i] * K >= ((size_t)1 << 26) &&
