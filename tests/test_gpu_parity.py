@@ -442,11 +442,13 @@ def test_lm_head_argmax_wide_rows(orc, M, V, K):
     assert ids_ref[M - 1] == 0 and np.isneginf(logits_ref[2, 33])
 
 
-def test_linear_wide_rows(orc):
-    """The 16-row tiles as a plain product (outputs only, no argmax): M = 9
-    against a 36000 x 2048 weight."""
-    M, N, K, gs = 9, 36000, 2048, 64
-    A, W, S = make_case(9200, M, N, K, gs)
+@pytest.mark.parametrize("M,N,K", [(9, 36000, 2048), (16, 65539, 1024), (7, 131075, 512)])
+def test_linear_wide_rows(orc, M, N, K):
+    """The 16-row tiles as a plain product (outputs only, no argmax): every
+    K the kernel takes (a tile of 8, 4 and 2 quads of 4 groups), ragged last
+    tiles."""
+    gs = 64
+    A, W, S = make_case(9200 + K, M, N, K, gs)
     assert_bits_equal(host(q.linear_i8(dev(A), dev(W), dev(S), gs)), orc.linear(A, W, S, gs), "C")
 
 
