@@ -794,6 +794,33 @@ __global__ __launch_bounds__(64 * NW, MINB) void gemm_mf_wide_kernel(const float
                                                       rW, row * K + 16 * c, 64 * (g0 + u), 0));
         wsr[sl] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rS, row * Kg * 4, 4 * g0, 0));
     };
+    // ---- quantize A into LDS (every thread of the block, before its
+    // barrier). A team of 4 lanes per (row, group), rows 0..RW-1, groups
+    // fastest (a wave's loads read 16 consecutive 256-byte groups, 64 bytes
+    // a team each); rows past M are zeros, and with RW = 8 rows 8..15 are
+    // zero-filled. Lane j of a team holds x[16v + 4j + c] (v, c = 0..3):
+    // the whole chains i = 4j + c of the sum of squares, t = v ascending.
+    // v_i = P_i + P_{i+8} pairs lanes j and j + 2, the tree's v_i + v_{i+4}
+    // lanes 0 and 1, then (s0 + s1) + (s2 + s3) in lane 0. The teams go in
+    // batches of QB passes whose loads are all issued before any of them is
+    // used (rows clamped into A, no branch around a load); the first batch
+    // goes out ahead of the weight stream, so waiting for it leaves the
+    // weights in flight.
+    const int RW = M <= 8 ? 8 : 16;
+    const int nteam = RW * Kg;  // a multiple of NT / 4 (Kg is a multiple of 8)
+    const int tj = tid & 3;
+    constexpr int QB = 4;
+    float4 xb[QB][4];
+    auto load_batch = [&](int tb) __attribute__((always_inline)) {
+#pragma unroll
+        for (int it = 0; it < QB; ++it) {
+            const int tm = min((tid >> 2) + tb + (NT / 4) * it, nteam - 1);
+            const float *xr = A + (size_t)min(tm / Kg, M - 1) * K + 64 * (tm % Kg) + 4 * tj;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) xb[it][v] = *reinterpret_cast<const float4 *>(xr + 16 * v);
+        }
+    };
+    load_batch(0);
     // the weight stream starts before the activations are quantized; the
     // slots are issued in ring order, as the loop reissues them (the wait
     // counts at the loop head cover both paths: any other order here would
@@ -806,15 +833,6 @@ __global__ __launch_bounds__(64 * NW, MINB) void gemm_mf_wide_kernel(const float
         }
         __builtin_amdgcn_sched_barrier(0);
     }
-    // ---- quantize A into LDS (every thread of the block, before its
-    // barrier). A team of 4 lanes per (row, group), rows 0..RW-1, groups
-    // fastest (a wave's loads read 16 consecutive 256-byte groups, 64 bytes
-    // a team each); rows past M are zeros, and with RW = 8 rows 8..15 are
-    // zero-filled. Lane j of a team holds x[16v + 4j + c] (v, c = 0..3):
-    // the whole chains i = 4j + c of the sum of squares, t = v ascending.
-    // v_i = P_i + P_{i+8} pairs lanes j and j + 2, the tree's v_i + v_{i+4}
-    // lanes 0 and 1, then (s0 + s1) + (s2 + s3) in lane 0.
-    const int RW = M <= 8 ? 8 : 16;
     if (RW == 8) {
         for (int q = tid; q < Kg * 16; q += NT) {  // (group, u, c) pieces of rows 8..15
             const int g = q >> 4, u = (q >> 3) & 1, cc = (q >> 1) & 3, r = 8 + 4 * (q & 1);
@@ -824,68 +842,81 @@ __global__ __launch_bounds__(64 * NW, MINB) void gemm_mf_wide_kernel(const float
         }
         for (int q = tid; q < Kg * 8; q += NT) asl[(q >> 3) * 16 + 8 + (q & 7)] = 0.0f;
     }
-    const int tj = tid & 3;
-    for (int tm = tid >> 2; tm < RW * Kg; tm += NT / 4) {
-        const int g = tm % Kg, m = tm / Kg;
-        const bool real = m < M;
-        float4 xv[4];
-        const float *xr = A + (size_t)min(m, M - 1) * K + 64 * g + 4 * tj;
+    // batch tb's teams (their loads in xb)
+    auto quant_batch = [&](int tb) __attribute__((always_inline)) {
 #pragma unroll
-        for (int v = 0; v < 4; ++v)
-            xv[v] = real ? *reinterpret_cast<const float4 *>(xr + 16 * v) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        float P[4];
-        P[0] = fmaf(xv[0].x, xv[0].x, 0.0f);
-        P[1] = fmaf(xv[0].y, xv[0].y, 0.0f);
-        P[2] = fmaf(xv[0].z, xv[0].z, 0.0f);
-        P[3] = fmaf(xv[0].w, xv[0].w, 0.0f);
-#pragma unroll
-        for (int v = 1; v < 4; ++v) {
-            P[0] = fmaf(xv[v].x, xv[v].x, P[0]);
-            P[1] = fmaf(xv[v].y, xv[v].y, P[1]);
-            P[2] = fmaf(xv[v].z, xv[v].z, P[2]);
-            P[3] = fmaf(xv[v].w, xv[v].w, P[3]);
-        }
-        float V[4], T[4];
-#pragma unroll
-        for (int c = 0; c < 4; ++c) V[c] = P[c] + __shfl_xor(P[c], 2, 4);  // lanes 0, 1: v_{4j+c}
-#pragma unroll
-        for (int c = 0; c < 4; ++c) T[c] = V[c] + __shfl_xor(V[c], 1, 4);  // lane 0: s_c
-        const float sumsq = __shfl((T[0] + T[1]) + (T[2] + T[3]), 0, 4);
-        const float sc = group_scale(sumsq, 1.0f / 64.0f);
-        const float inv = rcp_rn(sc);
-        // q = rne(x * inv): for a finite scale |q| <= 1016, and adding and
-        // removing 1.5 * 2^23 rounds to the integer, ties to even, exactly
-        // in fp16 (quant_pair_finite's integer); otherwise the saturating
-        // conversion of the reference, as int16 converted to fp16
-        uint32_t h[8];  // h[2v + e]: elements 16v + 4tj + 2e, +1
-        if (__builtin_expect(__builtin_isfinite(sc), 1)) {
-            constexpr float kMagic = 12582912.0f;
+        for (int it = 0; it < QB; ++it) {
+            const int tm = (tid >> 2) + tb + (NT / 4) * it;
+            if (tm >= nteam) break;  // wave-uniform (16 teams a wave)
+            const int g = tm % Kg, m = tm / Kg;
+            const bool real = m < M;
+            float4 xv[4];
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
-                const float r0 = (xv[v].x * inv + kMagic) - kMagic, r1 = (xv[v].y * inv + kMagic) - kMagic;
-                const float r2 = (xv[v].z * inv + kMagic) - kMagic, r3 = (xv[v].w * inv + kMagic) - kMagic;
-                h[2 * v] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(r0, r1));
-                h[2 * v + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(r2, r3));
+                const float4 f = xb[it][v];
+                xv[v] = real ? f : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
             }
-        } else {
+            float P[4];
+            P[0] = fmaf(xv[0].x, xv[0].x, 0.0f);
+            P[1] = fmaf(xv[0].y, xv[0].y, 0.0f);
+            P[2] = fmaf(xv[0].z, xv[0].z, 0.0f);
+            P[3] = fmaf(xv[0].w, xv[0].w, 0.0f);
 #pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                const uint32_t q0 = quant_pair(xv[v].x * inv, xv[v].y * inv);
-                const uint32_t q1 = quant_pair(xv[v].z * inv, xv[v].w * inv);
-                h[2 * v] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(
-                                                  (float)(int16_t)(q0 & 0xFFFF), (float)(int16_t)(q0 >> 16)));
-                h[2 * v + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(
-                                                      (float)(int16_t)(q1 & 0xFFFF), (float)(int16_t)(q1 >> 16)));
+            for (int v = 1; v < 4; ++v) {
+                P[0] = fmaf(xv[v].x, xv[v].x, P[0]);
+                P[1] = fmaf(xv[v].y, xv[v].y, P[1]);
+                P[2] = fmaf(xv[v].z, xv[v].z, P[2]);
+                P[3] = fmaf(xv[v].w, xv[v].w, P[3]);
             }
+            float V[4], T[4];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) V[c] = P[c] + __shfl_xor(P[c], 2, 4);  // lanes 0, 1: v_{4j+c}
+#pragma unroll
+            for (int c = 0; c < 4; ++c) T[c] = V[c] + __shfl_xor(V[c], 1, 4);  // lane 0: s_c
+            const float sumsq = __shfl((T[0] + T[1]) + (T[2] + T[3]), 0, 4);
+            const float sc = group_scale(sumsq, 1.0f / 64.0f);
+            const float inv = rcp_rn(sc);
+            // q = rne(x * inv): for a finite scale |q| <= 1016, and adding and
+            // removing 1.5 * 2^23 rounds to the integer, ties to even, exactly
+            // in fp16 (quant_pair_finite's integer); otherwise the saturating
+            // conversion of the reference, as int16 converted to fp16
+            uint32_t h[8];  // h[2v + e]: elements 16v + 4tj + 2e, +1
+            if (__builtin_expect(__builtin_isfinite(sc), 1)) {
+                constexpr float kMagic = 12582912.0f;
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const float r0 = (xv[v].x * inv + kMagic) - kMagic, r1 = (xv[v].y * inv + kMagic) - kMagic;
+                    const float r2 = (xv[v].z * inv + kMagic) - kMagic, r3 = (xv[v].w * inv + kMagic) - kMagic;
+                    h[2 * v] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(r0, r1));
+                    h[2 * v + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(r2, r3));
+                }
+            } else {
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const uint32_t q0 = quant_pair(xv[v].x * inv, xv[v].y * inv);
+                    const uint32_t q1 = quant_pair(xv[v].z * inv, xv[v].w * inv);
+                    h[2 * v] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(
+                                                      (float)(int16_t)(q0 & 0xFFFF), (float)(int16_t)(q0 >> 16)));
+                    h[2 * v + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(
+                                                          (float)(int16_t)(q1 & 0xFFFF), (float)(int16_t)(q1 >> 16)));
+                }
+            }
+            // elements 16v + 4tj + c are halves 4(tj % 2) + c of piece 2v + tj / 2,
+            // i.e. (u, lane c') = (tj / 2, 16v + m)
+            unsigned char *Ab = reinterpret_cast<unsigned char *>(Al);
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+                *reinterpret_cast<uint2 *>(Ab + ((g * 2 + (tj >> 1)) * 64 + 16 * v + m) * 16 + 8 * (tj & 1)) =
+                    real ? make_uint2(h[2 * v], h[2 * v + 1]) : make_uint2(0u, 0u);
+            if (tj == 0) asl[g * 16 + m] = real ? sc : 0.0f;
         }
-        // elements 16v + 4tj + c are halves 4(tj % 2) + c of piece 2v + tj / 2,
-        // i.e. (u, lane c') = (tj / 2, 16v + m)
-        unsigned char *Ab = reinterpret_cast<unsigned char *>(Al);
-#pragma unroll
-        for (int v = 0; v < 4; ++v)
-            *reinterpret_cast<uint2 *>(Ab + ((g * 2 + (tj >> 1)) * 64 + 16 * v + m) * 16 + 8 * (tj & 1)) =
-                real ? make_uint2(h[2 * v], h[2 * v + 1]) : make_uint2(0u, 0u);
-        if (tj == 0) asl[g * 16 + m] = real ? sc : 0.0f;
+    };
+    // the first batch straight-line: its loads went out before the weight
+    // ring's, and this code's wait for them leaves the ring in flight
+    quant_batch(0);
+    for (int tb = QB * (NT / 4); tb < nteam; tb += QB * (NT / 4)) {
+        load_batch(tb);
+        quant_batch(tb);
     }
     __syncthreads();
     if (nq == 0) {  // no tile for this wave: an empty partial (no barrier follows)
