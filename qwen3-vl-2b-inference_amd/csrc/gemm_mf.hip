@@ -32,7 +32,7 @@
 //   holds a_s of rows 32t + 8(e/4) + 4(l/32) + e%4, the rows a lane's 16
 //   accumulators hold.
 // * B: the block loads its weight rows (64 bytes per row and group) once,
-//   widens them to fp16 (0x64xx exponent trick) and stores them in LDS in the
+//   widens them to fp16 (one SDWA conversion a byte) and stores them in LDS in the
 //   same fragment order, two buffers deep, so every wave reads its B
 //   fragments with one ds_read_b128 per slice and n-tile. The 16-byte slots
 //   are swizzled (slot ^ 4*(s/2) ^ 8*(l/32)) so that the writers' and the
@@ -143,15 +143,17 @@ hipError_t launch_quantize_frag(const float *A, _Float16 *qf, float *asf, int M,
 }
 
 // ---------------------------------------------------------------- the GEMM
-// 4 bytes (already xor 0x80) -> 4 fp16 values in two dwords:
-// half(0x6400 | b') - 1152 = b' - 128 = b.
+// 4 int8 bytes -> 4 fp16 values in two dwords (bytes 0, 1 -> lo, 2, 3 -> hi),
+// one conversion per byte: v_cvt_f16_i16 reading the byte sign-extended
+// (SDWA source select) and writing one half of the destination (the other
+// half kept), exact for every int8.
 __device__ __forceinline__ void widen4_mf(uint32_t x, uint32_t &lo, uint32_t &hi) {
-    const uint32_t e = 0x64646464u;
-    const uint32_t l = __builtin_amdgcn_perm(e, x, 0x04010400u);
-    const uint32_t hh = __builtin_amdgcn_perm(e, x, 0x04030402u);
-    const half2_t off = {(_Float16)1152.0f, (_Float16)1152.0f};
-    lo = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, l) - off);
-    hi = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, hh) - off);
+    asm("v_cvt_f16_i16_sdwa %0, sext(%2) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_0\n\t"
+        "v_cvt_f16_i16_sdwa %0, sext(%2) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_1\n\t"
+        "v_cvt_f16_i16_sdwa %1, sext(%2) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_2\n\t"
+        "v_cvt_f16_i16_sdwa %1, sext(%2) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_3"
+        : "=&v"(lo), "=&v"(hi)
+        : "v"(x));
 }
 
 // Swizzled 16-byte slot of (slice s, lane l) inside an n-tile's 4 KB.
@@ -369,7 +371,7 @@ __global__ __launch_bounds__(256, BPC) void gemm_mf_kernel(
         unsigned char *Bs = smem + (g & 1) * BBUF;
 #pragma unroll
         for (int i = 0; i < BCH; ++i) {
-            const u32x4 v = braw[sl][i] ^ (u32x4){0x80808080u, 0x80808080u, 0x80808080u, 0x80808080u};
+            const u32x4 v = braw[sl][i];
             uint32_t w[8];
             widen4_mf(v.x, w[0], w[1]);
             widen4_mf(v.y, w[2], w[3]);
@@ -740,7 +742,7 @@ hipError_t launch_gemm_mf(const GemmMfArgs &a, bool swiglu, int cus, hipStream_t
 // weights going straight from the load into the MFMA operand:
 // * B (weights): lane l takes weight row n = l % 16 of the tile and, of each
 //   group's 64 bytes, bytes 16c .. 16c + 15 (c = l / 16) -- one 16-byte load a
-//   lane and group; widened to fp16 (0x64xx trick), its first 8 k feed the
+//   lane and group; widened to fp16 (widen4_mf), its first 8 k feed the
 //   group's first MFMA, the other 8 the second.
 // * A: MFMA u of lane l takes row l % 16, k = 16c + 8u + j (j = 0..7) -- the k
 //   the weight bytes hold. Each block quantizes the activations itself into
@@ -939,7 +941,7 @@ __global__ __launch_bounds__(64 * NW, MINB) void gemm_mf_wide_kernel(const float
         half8_t bf[4][2];
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-            const u32x4 v = wr[sl][u] ^ (u32x4){0x80808080u, 0x80808080u, 0x80808080u, 0x80808080u};
+            const u32x4 v = wr[sl][u];
             uint32_t w[8];
             widen4_mf(v.x, w[0], w[1]);
             widen4_mf(v.y, w[2], w[3]);
