@@ -905,17 +905,22 @@ __global__ __launch_bounds__(PV_THREADS) void attn_softmax_pv_kernel(
             const float *vrow = vt + rl * PV_RS;
             const int len = min(PV_TC, n - t0);
             float4 Ae, Be, Av[16], Bv[16];
-            auto ld = [&](float4 &E, float4 *V, int tb) {
-                E = *reinterpret_cast<const float4 *>(eph + tb + 4 * rl);
+            // the LDS reads of a batch: its e (part 0) and V[k .. k+3]
+            auto ldpart = [&](float4 &E, float4 *V, int tb, int k) {
+                if (k == 0) E = *reinterpret_cast<const float4 *>(eph + tb + 4 * rl);
 #pragma unroll
-                for (int u = 0; u < 16; ++u) V[u] = *reinterpret_cast<const float4 *>(vrow + tb + 4 * u);
+                for (int u = k; u < k + 4; ++u) V[u] = *reinterpret_cast<const float4 *>(vrow + tb + 4 * u);
             };
             // a head whose sum is not finite and positive has invh = 0 (a
             // finite positive sum is at most n, so its inverse is not 0):
             // the reference zeroes its p (text_layer.cpp:512-515), and e * 0
             // would be NaN for an e of -inf
             const bool live = invh > 0.0f;
-            auto run64 = [&](const float4 &E, const float4 *V, int tb, auto last_c) {
+            // pre(k) issues part k of the next batch's reads before block k
+            // of 16 steps: spread over the steps, the reads enter the LDS
+            // queue while the chain runs instead of holding its first step
+            // back until all of them are issued
+            auto run64 = [&](const float4 &E, const float4 *V, int tb, auto last_c, auto pre) {
                 float p0, p1, p2, p3;
                 if constexpr (decltype(last_c)::value) {
                     const int t = tb + 4 * rl;
@@ -935,40 +940,43 @@ __global__ __launch_bounds__(PV_THREADS) void attn_softmax_pv_kernel(
                     // the last batch stops at the first block of 16 steps
                     // wholly past the context (their p are 0: no change)
                     if (decltype(last_c)::value && tb + 4 * k >= len) break;  // uniform
+                    pre(k);
+                    __builtin_amdgcn_sched_barrier(0);
                     fmac16_row_bcast(acc, p0, p1, p2, p3, V + k, k);
+                    __builtin_amdgcn_sched_barrier(0);
                 }
             };
             const std::integral_constant<bool, false> full{};
             const std::integral_constant<bool, true> last{};
+            auto none = [](int) {};
             // batches of 64 in two register sets used in turn: the next
-            // batch's LDS reads are issued before the current batch's
-            // steps; batches 0 .. nbat-2 are whole, nbat-1 the last
+            // batch's LDS reads go out during the current batch's steps
+            // (every read of the set in use has completed before its first
+            // step); batches 0 .. nbat-2 are whole, nbat-1 the last
             const int nbat = (len + 63) >> 6, nfull = nbat - 1;
-            ld(Ae, Av, 0);
+#pragma unroll
+            for (int k = 0; k < 16; k += 4) ldpart(Ae, Av, 0, k);
             int bi = 0;
             for (; bi + 2 <= nfull; bi += 2) {
                 lgkm_wait0();
                 __builtin_amdgcn_sched_barrier(0);
-                ld(Be, Bv, 64 * (bi + 1));
-                run64(Ae, Av, 64 * bi, full);
-                __builtin_amdgcn_sched_barrier(0);
+                run64(Ae, Av, 64 * bi, full, [&](int k) { ldpart(Be, Bv, 64 * (bi + 1), k); });
                 lgkm_wait0();
                 __builtin_amdgcn_sched_barrier(0);
-                ld(Ae, Av, 64 * (bi + 2));  // bi + 2 <= nfull < nbat
-                run64(Be, Bv, 64 * (bi + 1), full);
-                __builtin_amdgcn_sched_barrier(0);
+                // bi + 2 <= nfull < nbat
+                run64(Be, Bv, 64 * (bi + 1), full, [&](int k) { ldpart(Ae, Av, 64 * (bi + 2), k); });
             }
             if (bi < nfull) {  // A holds whole batch bi, the last is bi + 1
                 lgkm_wait0();
                 __builtin_amdgcn_sched_barrier(0);
-                ld(Be, Bv, 64 * (bi + 1));
-                run64(Ae, Av, 64 * bi, full);
-                __builtin_amdgcn_sched_barrier(0);
+                run64(Ae, Av, 64 * bi, full, [&](int k) { ldpart(Be, Bv, 64 * (bi + 1), k); });
                 lgkm_wait0();
-                run64(Be, Bv, 64 * (bi + 1), last);
+                __builtin_amdgcn_sched_barrier(0);
+                run64(Be, Bv, 64 * (bi + 1), last, none);
             } else {  // A holds the last batch
                 lgkm_wait0();
-                run64(Ae, Av, 64 * bi, last);
+                __builtin_amdgcn_sched_barrier(0);
+                run64(Ae, Av, 64 * bi, last, none);
             }
         }
     }
