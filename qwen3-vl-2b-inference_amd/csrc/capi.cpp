@@ -291,7 +291,9 @@ int run_linear(const float *A, int nseg, const int8_t *const *W, const float *co
                     pv = reinterpret_cast<float *>(wbase + LG.parts_val);
                     pi = reinterpret_cast<int32_t *>(wbase + LG.parts_idx);
                     nparts = gemm_mf_wide_parts((int)Ns[i], cus);
-                    if ((size_t)nparts > kMaxGemvParts) return Q3VL_ERR_UNSUPPORTED;
+                    if ((size_t)nparts > kMaxGemvParts)
+                        return fail(Q3VL_ERR_UNSUPPORTED, "argmax: %d partials exceed %zu", nparts,
+                                    kMaxGemvParts);
                 }
                 Q3VL_HIP(launch_gemm_mf_wide(A, W[i], S[i], C[i], (int)M, (int)Ns[i], (int)K, pv, pi, cus, st),
                          "wide gemm launch");
@@ -316,7 +318,9 @@ int run_linear(const float *A, int nseg, const int8_t *const *W, const float *co
                 g.part_idx = reinterpret_cast<int32_t *>(wbase + LG.parts_idx);
                 const int cols = gemm_mf_argmax_cols((int)M);
                 nparts = (int)((Ns[i] + cols - 1) / cols);
-                if ((size_t)nparts > kMaxGemvParts) return Q3VL_ERR_UNSUPPORTED;
+                if ((size_t)nparts > kMaxGemvParts)
+                    return fail(Q3VL_ERR_UNSUPPORTED, "argmax: %d partials exceed %zu", nparts,
+                                kMaxGemvParts);
             }
             Q3VL_HIP(launch_gemm_mf(g, false, cus, st), "gemm launch");
             if (mode == GEMV_ARGMAX)
